@@ -1,0 +1,131 @@
+/*
+ * libllmoe -- LLaDA2 routed-expert MoE layer on MI355X (gfx950), C ABI.
+ *
+ * One layer object holds one MoE layer's expert weights (routed experts 0..E-1 plus an optional shared expert
+ * at index E) resident in HBM, its router, and a workspace sized for `max_tokens` tokens. Every compute call
+ * takes DEVICE pointers, is asynchronous on the given HIP stream (NULL = the default stream), performs no host
+ * synchronisation, no allocation and no memset, and is therefore capturable in a HIP graph. Work-item counts
+ * are produced and consumed on the device.
+ *
+ * Errors: every call returns LLMOE_OK (0) or a negative LLMOE_E* code; llmoe_last_error() returns the message
+ * of the calling thread's last failure. Nothing exits the process.
+ *
+ * Threading: a layer object is not thread-safe (its workspace is shared by its calls); serialise calls per
+ * layer, as the reference serialises llada_generate with a mutex (engine/libllada.cu:30). Distinct layer
+ * objects may be used concurrently on distinct streams.
+ *
+ * Reference interfaces replaced (patrickbdevaney/llada2-orin-cuda; the reference exposes the MoE path as
+ * in-process C++ below its whole-model C ABI engine/libllada.cu:13-52):
+ *   llmoe_layer_create    Engine::load's expert part: ExpertTable + relayout_matrix (engine/engine.cu:206-224,
+ *                         engine/moe_i8.cu:48-53, :93-121)
+ *   llmoe_quantize_a8     ops::quant_rows_q8 / quant_row_smem (engine/ops.cu:40-66, :127-135)
+ *   llmoe_route           ops::router_mma + ops::route_schedule / route_batch_select/plan/place
+ *                         (engine/ops.cu:137-205, :223-423)
+ *   llmoe_dispatch        the host counting sort of engine/tests/test_moe_i8.cu:73-98 (externally routed)
+ *   llmoe_experts         gemm<..,0> -> fwht512_q8 -> gemm<..,1> -> combine (engine/engine.cu:461-478,
+ *                         engine/moe_i8.cu:408-515)
+ *   llmoe_layer_forward   the MoE half of Engine::layer_step / Engine::prefill (engine/engine.cu:445-479,
+ *                         :616-649), without the norm/rotation before it and the un-rotation after it
+ */
+#ifndef LLMOE_H
+#define LLMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LLMOE_OK 0
+#define LLMOE_EINVAL (-1)   /* bad argument or shape */
+#define LLMOE_ENOMEM (-2)   /* device or host allocation failed */
+#define LLMOE_EHIP (-3)     /* a HIP runtime call failed */
+#define LLMOE_ESTATE (-4)   /* call order: llmoe_experts before llmoe_route / llmoe_dispatch for this T */
+
+typedef struct llmoe_layer llmoe_layer;
+typedef void* llmoe_stream; /* hipStream_t */
+
+typedef struct {
+    int hidden;          /* H, multiple of 512 (2048 in LLaDA2.2-mini) */
+    int inter;           /* I, must be 512 (FWHT-512 on the down input) */
+    int n_experts;       /* E routed experts, <= 256 */
+    int top_k;           /* K experts per token, <= 8 */
+    int pool;            /* C: per-block expert pool (48 shipped, engine/ops.cu:257); >= E disables it */
+    int block;           /* tokens per routing block (32, the diffusion block); <= 32 */
+    float routed_scale;  /* w = score / sum(score) * routed_scale (2.5, engine/engine.cu:142) */
+    int has_shared;      /* expert index E is a shared expert, applied to every token with weight 1 */
+    int max_tokens;      /* workspace capacity in tokens */
+} llmoe_layer_desc;
+
+/* Create a layer from packlib format-"i8" expert matrices (quant/packlib.py:140-197) in HOST memory.
+ *   blob            packed matrices; gate_up of expert e at gu_off[e] ([2I, H], rows permuted by gu_row_perm,
+ *                   quant/packlib.py:98-102), down at d_off[e] ([H, I])
+ *   gu_off, d_off   [E + has_shared] byte offsets into blob
+ *   bits            [E + has_shared] 2, 3, 4 or 8
+ *   router_w        [H, E] fp32 router matrix (k-major), or NULL (then only logits routing is available)
+ *   router_bias     [E] fp32 expert bias (required)
+ * The library copies the weights to HBM and rewrites them in place into its MFMA operand layout. */
+int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t blob_bytes, const uint64_t* gu_off,
+                       const uint64_t* d_off, const int8_t* bits, const float* router_w, const float* router_bias,
+                       llmoe_layer** out);
+int llmoe_layer_destroy(llmoe_layer* layer);
+
+/* A8: x fp32 [rows, cols] -> q int8 [rows, cols] (logical column order), s fp32 [rows, cols/128],
+ * sum int32 [rows, cols/128]; symmetric per (row, 128-group), s = max(max|x| / 127, 1e-30),
+ * q = clamp(rint(x / s), +-127). cols % 512 == 0. */
+int llmoe_quantize_a8(const float* x, int rows, int cols, int8_t* q, float* s, int32_t* sum, llmoe_stream stream);
+
+/* Routing + dispatch for T tokens. Exactly one of x (fp32 [T, H], router input: logits = x Wr) and logits
+ * (fp32 [T, E]) is non-NULL. Results stay in the layer workspace (llmoe_layer_buffers). */
+int llmoe_route(llmoe_layer* layer, const float* x, const float* logits, int T, llmoe_stream stream);
+
+/* Dispatch for externally routed tokens: topk int32 [T, K] (K DISTINCT experts per token), topw fp32 [T, K]. */
+int llmoe_dispatch(llmoe_layer* layer, const int32_t* topk, const float* topw, int T, llmoe_stream stream);
+
+/* Expert stage for the routing last set for the same T: gate_up -> FWHT-512 + A8 -> down -> combine.
+ * xq/xs/xsum: A8 activations of the T tokens (llmoe_quantize_a8 layout). out: fp32 [T, H]
+ *   out[t] = sum_k w[t,k] expert_k(x_t) (+ shared(x_t)), summed in rank order, shared last. */
+int llmoe_experts(llmoe_layer* layer, const int8_t* xq, const float* xs, const int32_t* xsum, int T, float* out,
+                  llmoe_stream stream);
+
+/* Whole layer: A8(x) -> route (x Wr, or the given logits) -> experts -> out. x fp32 [T, H]. */
+int llmoe_layer_forward(llmoe_layer* layer, const float* x, const float* logits, int T, float* out,
+                        llmoe_stream stream);
+
+/* Device pointers of the layer workspace (valid until destroy), for inspection and tests. Slot s in
+ * [0, T K) is a routed (token, expert) pair, expert-major then token-ascending; slot T K + t is token t's
+ * shared-expert slot. */
+typedef struct {
+    int8_t* xq; float* xs; int32_t* xsum;              /* A8 of the layer input        [T, H], [T, H/128] */
+    float* logits_part;                                /* router partials              [8, T, E] */
+    int32_t* topk; float* topw;                        /*                              [T, K] */
+    int32_t* count; int32_t* start;                    /* slots per routed expert      [E] */
+    int32_t* slot_token; float* slot_weight;           /*                              [S] */
+    int32_t* tok_slots;                                /* [T, K + 1] (last: shared slot, -1 if none) */
+    int32_t* items; int32_t* n_items;                  /* work items {expert, slot0, ntok, 0} */
+    uint16_t* Z;                                       /* fp16 SiLU(g) u               [S, I] */
+    int8_t* zq; float* zs; int32_t* zsum;              /* A8(Z H512)                   [S, I], [S, I/128] */
+    float* Y;                                          /* weighted expert outputs      [S, H] */
+    int ntok;                                          /* tokens per work item of the last dispatch */
+    int max_items;                                     /* work-item capacity of the last dispatch */
+} llmoe_buffers;
+int llmoe_layer_buffers(const llmoe_layer* layer, llmoe_buffers* out);
+
+/* Expert weight bytes resident in HBM (the weight-stream bytes of a full pass over every expert). */
+int llmoe_layer_weight_bytes(const llmoe_layer* layer, size_t* bytes);
+
+/* Exact int32 group products of one expert matrix (test entry; the same MFMA core as llmoe_experts):
+ *   P[n, r, g] = sum_{k in group g} code[r, k] xq[n, k] - zero[r, g] xsum[n, g]
+ * which: 0 = gate_up ([2I, H], r in packlib row order), 1 = down ([H, I]). xq int8 [n, Kw], xsum [n, Kw/128],
+ * n <= 64. P int32 [n, R, Kw/128]. */
+int llmoe_group_products(llmoe_layer* layer, int expert, int which, const int8_t* xq, const int32_t* xsum, int n,
+                         int32_t* P, llmoe_stream stream);
+
+/* Message of the calling thread's last error ("" if none). */
+const char* llmoe_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,395 @@
+// libllmoe C ABI (include/llmoe.h): layer construction, workspace, and the launch sequence of the MoE layer
+//   A8(x) -> router logits -> route (pool, top-K, weights) -> plan + place (slots, work items)
+//   -> gate_up GEMM -> FWHT-512 + A8 -> down GEMM -> combine
+// everything asynchronous on the caller's stream (engine/engine.cu:445-479 is the reference sequence).
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "llmoe.h"
+#include "llmoe_internal.h"
+
+using namespace llmoe;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIPCHECK(expr)                                                                                     \
+    do {                                                                                                   \
+        const hipError_t e_ = (expr);                                                                      \
+        if (e_ != hipSuccess) return fail(LLMOE_EHIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_),      \
+                                          __FILE__, __LINE__);                                             \
+    } while (0)
+
+int tile_wbytes(int bits) { return bits == 8 ? 2048 : bits == 4 ? 1024 : bits == 3 ? 768 : bits == 2 ? 512 : -1; }
+size_t packlib_matrix_bytes(int R, int K, int bits) {
+    return size_t(R / 16) * size_t(K / GROUP) * size_t(tile_wbytes(bits) + 48);
+}
+
+hipError_t g_setup = hipErrorNotInitialized;
+bool g_setup_done = false;
+
+}  // namespace
+
+struct llmoe_layer {
+    llmoe_layer_desc d{};
+    int nexp = 0;                                   // E + has_shared
+    uint8_t* arena = nullptr;
+    size_t arena_bytes = 0;
+    size_t weight_bytes = 0;                        // distinct matrices
+    uint64_t* gu_off_d = nullptr;
+    uint64_t* d_off_d = nullptr;
+    int8_t* bits_d = nullptr;
+    float* router_w = nullptr;
+    float* bias = nullptr;
+    // workspace
+    int8_t* xq = nullptr; float* xs = nullptr; int32_t* xsum = nullptr;
+    float* part = nullptr;
+    int32_t* topk = nullptr; float* topw = nullptr;
+    uint32_t* mask = nullptr; int32_t* bpre = nullptr;
+    int32_t* count = nullptr; int32_t* start = nullptr;
+    Item* items = nullptr; int* n_items = nullptr;
+    int32_t* slot_token = nullptr; float* slot_weight = nullptr; int32_t* tok_slots = nullptr;
+    uint16_t* Z = nullptr; int8_t* zq = nullptr; float* zs = nullptr; int32_t* zsum = nullptr;
+    float* Y = nullptr;
+    Item* p_item = nullptr; int* p_count = nullptr;  // single-item list of llmoe_group_products
+    Item p_item_host{}; int p_count_host = 1;
+    size_t items_cap = 0;
+    // routing state
+    int routed_T = -1, ntok = 16, max_items = 0;
+    std::vector<void*> allocs;
+
+    template <class T>
+    hipError_t alloc(T** p, size_t count_) {
+        void* v = nullptr;
+        const hipError_t e = hipMalloc(&v, std::max<size_t>(count_ * sizeof(T), 16));
+        if (e == hipSuccess) {
+            allocs.push_back(v);
+            *p = static_cast<T*>(v);
+        }
+        return e;
+    }
+    ~llmoe_layer() {
+        for (void* p : allocs) (void)hipFree(p);
+    }
+};
+
+namespace {
+
+int check_layer(const llmoe_layer* L) {
+    if (!L) return fail(LLMOE_EINVAL, "null layer");
+    return LLMOE_OK;
+}
+
+int nblocks(const llmoe_layer* L, int T) { return (T + L->d.block - 1) / L->d.block; }
+
+// tokens per work item and the item capacity for T tokens
+void choose_items(llmoe_layer* L, int T) {
+    const auto& d = L->d;
+    const long eff = std::min<long>(d.n_experts, long(nblocks(L, T)) * std::min(d.pool, d.n_experts));
+    const long avg = (long(T) * d.top_k + eff - 1) / eff;
+    const int nt = avg <= 8 ? 1 : avg <= 24 ? 2 : 4;
+    L->ntok = 16 * nt;
+    const long routed = eff + (long(T) * d.top_k + L->ntok - 1) / L->ntok;
+    const long shared = d.has_shared ? (T + L->ntok - 1) / L->ntok : 0;
+    L->max_items = int(routed + shared);
+}
+
+int check_T(const llmoe_layer* L, int T) {
+    if (T < 1 || T > L->d.max_tokens) return fail(LLMOE_EINVAL, "T = %d outside [1, max_tokens = %d]", T, L->d.max_tokens);
+    return LLMOE_OK;
+}
+
+int plan_and_place(llmoe_layer* L, const int32_t* topk, const float* topw, int T, hipStream_t st) {
+    const auto& d = L->d;
+    choose_items(L, T);
+    if (size_t(L->max_items) > L->items_cap) return fail(LLMOE_EINVAL, "item capacity exceeded");
+    HIPCHECK(launch_plan(L->mask, T, d.n_experts, d.top_k, d.block, d.has_shared, L->ntok, L->count, L->start, L->bpre,
+                         L->items, L->n_items, st));
+    HIPCHECK(launch_place(topk, topw, L->mask, L->bpre, T, d.n_experts, d.top_k, d.block, d.has_shared,
+                          L->slot_token, L->slot_weight, L->tok_slots, st));
+    L->routed_T = T;
+    return LLMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* llmoe_last_error(void) { return g_err.c_str(); }
+
+int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t blob_bytes, const uint64_t* gu_off,
+                       const uint64_t* d_off, const int8_t* bits, const float* router_w, const float* router_bias,
+                       llmoe_layer** out) {
+    if (!desc || !blob || !gu_off || !d_off || !bits || !router_bias || !out)
+        return fail(LLMOE_EINVAL, "null argument");
+    *out = nullptr;
+    const llmoe_layer_desc d = *desc;
+    if (d.hidden != 2048) return fail(LLMOE_EINVAL, "hidden = %d: this build's GEMM geometry is H = 2048", d.hidden);
+    if (d.inter != 512) return fail(LLMOE_EINVAL, "inter = %d: FWHT-512 needs I = 512", d.inter);
+    if (d.n_experts < 64 || d.n_experts > 256 || d.n_experts % 64)
+        return fail(LLMOE_EINVAL, "n_experts = %d: need 64 <= E <= 256, E %% 64 == 0", d.n_experts);
+    if (d.top_k < 1 || d.top_k > 8 || d.top_k > d.n_experts) return fail(LLMOE_EINVAL, "top_k = %d", d.top_k);
+    if (d.pool < d.top_k) return fail(LLMOE_EINVAL, "pool = %d < top_k", d.pool);
+    if (d.block < 1 || d.block > 32) return fail(LLMOE_EINVAL, "block = %d outside [1, 32]", d.block);
+    if (d.max_tokens < 1) return fail(LLMOE_EINVAL, "max_tokens = %d", d.max_tokens);
+    const int nexp = d.n_experts + (d.has_shared ? 1 : 0);
+    const int H = d.hidden, I = d.inter;
+    // validate every matrix against the blob
+    std::vector<std::pair<uint64_t, size_t>> mats;
+    for (int e = 0; e < nexp; ++e) {
+        const int b = bits[e];
+        if (tile_wbytes(b) < 0) return fail(LLMOE_EINVAL, "expert %d: bits = %d (need 2, 3, 4 or 8)", e, b);
+        const size_t gb = packlib_matrix_bytes(2 * I, H, b), db = packlib_matrix_bytes(H, I, b);
+        if (gu_off[e] % 16 || d_off[e] % 16) return fail(LLMOE_EINVAL, "expert %d: offsets must be 16-byte aligned", e);
+        if (gu_off[e] + gb > blob_bytes || d_off[e] + db > blob_bytes)
+            return fail(LLMOE_EINVAL, "expert %d: matrix beyond the blob (%zu bytes)", e, blob_bytes);
+    }
+    if (!g_setup_done) {
+        g_setup = gemm_setup();
+        g_setup_done = true;
+    }
+    if (g_setup != hipSuccess) return fail(LLMOE_EHIP, "gemm_setup: %s", hipGetErrorString(g_setup));
+
+    llmoe_layer* L = new (std::nothrow) llmoe_layer();
+    if (!L) return fail(LLMOE_ENOMEM, "host allocation");
+    L->d = d;
+    L->nexp = nexp;
+    auto bail = [&](int code) {
+        delete L;
+        return code;
+    };
+#define ALLOC(ptr, n)                                                                                       \
+    do {                                                                                                    \
+        if (L->alloc(&(ptr), (n)) != hipSuccess) return bail(fail(LLMOE_ENOMEM, "hipMalloc %s", #ptr));     \
+    } while (0)
+    // weights: upload the packlib blob to a staging buffer, relayout every distinct matrix into the arena at
+    // the same offset (the device layout has the packlib byte count)
+    L->arena_bytes = blob_bytes;
+    ALLOC(L->arena, blob_bytes);
+    uint8_t* staging = nullptr;
+    if (hipMalloc(&staging, blob_bytes) != hipSuccess) return bail(fail(LLMOE_ENOMEM, "hipMalloc staging"));
+    int rc = LLMOE_OK;
+    do {
+        hipError_t e = hipMemcpy(staging, blob, blob_bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) { rc = fail(LLMOE_EHIP, "upload: %s", hipGetErrorString(e)); break; }
+        std::set<uint64_t> done;
+        for (int x = 0; x < nexp && rc == LLMOE_OK; ++x) {
+            const int b = bits[x];
+            for (int which = 0; which < 2; ++which) {
+                const uint64_t off = which == 0 ? gu_off[x] : d_off[x];
+                const int R = which == 0 ? 2 * I : H, K = which == 0 ? H : I;
+                if (done.count(off)) continue;   // an aliased entry is laid out once
+                done.insert(off);
+                L->weight_bytes += packlib_matrix_bytes(R, K, b);
+                e = launch_relayout(staging + off, L->arena + off, R, K, b, which == 0, nullptr);
+                if (e != hipSuccess) { rc = fail(LLMOE_EHIP, "relayout: %s", hipGetErrorString(e)); break; }
+            }
+        }
+        if (rc != LLMOE_OK) break;
+        e = hipDeviceSynchronize();
+        if (e != hipSuccess) rc = fail(LLMOE_EHIP, "relayout sync: %s", hipGetErrorString(e));
+    } while (0);
+    (void)hipFree(staging);
+    if (rc != LLMOE_OK) return bail(rc);
+
+    ALLOC(L->gu_off_d, nexp);
+    ALLOC(L->d_off_d, nexp);
+    ALLOC(L->bits_d, nexp);
+    ALLOC(L->bias, d.n_experts);
+    if (hipMemcpy(L->gu_off_d, gu_off, nexp * sizeof(uint64_t), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(L->d_off_d, d_off, nexp * sizeof(uint64_t), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(L->bits_d, bits, nexp, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(L->bias, router_bias, d.n_experts * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+        return bail(fail(LLMOE_EHIP, "table upload"));
+    if (router_w) {
+        ALLOC(L->router_w, size_t(H) * d.n_experts);
+        if (hipMemcpy(L->router_w, router_w, size_t(H) * d.n_experts * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+            return bail(fail(LLMOE_EHIP, "router upload"));
+    }
+    // workspace
+    const size_t Tm = size_t(d.max_tokens), K = size_t(d.top_k), E = size_t(d.n_experts);
+    const size_t S = Tm * (K + 1), nbm = (Tm + d.block - 1) / d.block;
+    ALLOC(L->xq, Tm * H);
+    ALLOC(L->xs, Tm * (H / GROUP));
+    ALLOC(L->xsum, Tm * (H / GROUP));
+    ALLOC(L->part, size_t(ROUTER_KC) * Tm * E);
+    ALLOC(L->topk, Tm * K);
+    ALLOC(L->topw, Tm * K);
+    ALLOC(L->mask, nbm * E);
+    ALLOC(L->bpre, nbm * E);
+    ALLOC(L->count, E);
+    ALLOC(L->start, E);
+    L->items_cap = E + (Tm * K + 15) / 16 + (Tm + 15) / 16 + 2;
+    ALLOC(L->items, L->items_cap);
+    ALLOC(L->n_items, 1);
+    ALLOC(L->slot_token, S);
+    ALLOC(L->slot_weight, S);
+    ALLOC(L->tok_slots, Tm * (K + 1));
+    ALLOC(L->Z, S * I);
+    ALLOC(L->zq, S * I);
+    ALLOC(L->zs, S * (I / GROUP));
+    ALLOC(L->zsum, S * (I / GROUP));
+    ALLOC(L->Y, S * H);
+    ALLOC(L->p_item, 1);
+    ALLOC(L->p_count, 1);
+#undef ALLOC
+    *out = L;
+    g_err.clear();
+    return LLMOE_OK;
+}
+
+int llmoe_layer_destroy(llmoe_layer* layer) {
+    if (!layer) return LLMOE_OK;
+    const hipError_t e = hipDeviceSynchronize();
+    delete layer;
+    if (e != hipSuccess) return fail(LLMOE_EHIP, "destroy sync: %s", hipGetErrorString(e));
+    return LLMOE_OK;
+}
+
+int llmoe_quantize_a8(const float* x, int rows, int cols, int8_t* q, float* s, int32_t* sum, llmoe_stream stream) {
+    if (!x || !q || !s || !sum) return fail(LLMOE_EINVAL, "null argument");
+    if (rows < 0 || cols <= 0 || cols % 512) return fail(LLMOE_EINVAL, "A8 shape %d x %d (cols %% 512 == 0)", rows, cols);
+    HIPCHECK(launch_quant_a8(x, rows, cols, q, s, sum, static_cast<hipStream_t>(stream)));
+    return LLMOE_OK;
+}
+
+int llmoe_route(llmoe_layer* L, const float* x, const float* logits, int T, llmoe_stream stream) {
+    if (int rc = check_layer(L)) return rc;
+    if (int rc = check_T(L, T)) return rc;
+    if ((x == nullptr) == (logits == nullptr)) return fail(LLMOE_EINVAL, "exactly one of x and logits must be given");
+    const auto& d = L->d;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    L->routed_T = -1;
+    const float* part = logits;
+    int nchunks = 1;
+    if (x) {
+        if (!L->router_w) return fail(LLMOE_EINVAL, "layer created without a router matrix");
+        HIPCHECK(launch_router_logits(x, L->router_w, T, d.hidden, d.n_experts, L->part, st));
+        part = L->part;
+        nchunks = ROUTER_KC;
+    }
+    HIPCHECK(launch_route(part, nchunks, L->bias, T, d.n_experts, d.top_k, d.pool, d.block, d.routed_scale, L->topk,
+                          L->topw, L->mask, st));
+    return plan_and_place(L, L->topk, L->topw, T, st);
+}
+
+int llmoe_dispatch(llmoe_layer* L, const int32_t* topk, const float* topw, int T, llmoe_stream stream) {
+    if (int rc = check_layer(L)) return rc;
+    if (int rc = check_T(L, T)) return rc;
+    if (!topk || !topw) return fail(LLMOE_EINVAL, "null argument");
+    const auto& d = L->d;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    L->routed_T = -1;
+    HIPCHECK(hipMemcpyAsync(L->topk, topk, size_t(T) * d.top_k * sizeof(int32_t), hipMemcpyDeviceToDevice, st));
+    HIPCHECK(hipMemcpyAsync(L->topw, topw, size_t(T) * d.top_k * sizeof(float), hipMemcpyDeviceToDevice, st));
+    HIPCHECK(launch_masks(L->topk, T, d.n_experts, d.top_k, d.block, L->mask, st));
+    return plan_and_place(L, L->topk, L->topw, T, st);
+}
+
+int llmoe_experts(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_t* xsum, int T, float* out,
+                  llmoe_stream stream) {
+    if (int rc = check_layer(L)) return rc;
+    if (!xq || !xs || !xsum || !out) return fail(LLMOE_EINVAL, "null argument");
+    if (T != L->routed_T) return fail(LLMOE_ESTATE, "no routing for T = %d (route or dispatch first)", T);
+    const auto& d = L->d;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const int H = d.hidden, I = d.inter, K = d.top_k;
+    const int S = T * K + (d.has_shared ? T : 0);
+    const int nt = L->ntok / 16;
+    GemmArgs g{};
+    g.base = L->arena;
+    g.bits = L->bits_d;
+    g.items = L->items;
+    g.n_items = L->n_items;
+    g.slot_weight = L->slot_weight;
+    // gate_up: B rows are token rows of x'
+    g.off = L->gu_off_d;
+    g.slot_token = L->slot_token;
+    g.xq = xq; g.xs = xs; g.xsum = xsum;
+    g.K = H; g.R = 2 * I; g.Z = L->Z;
+    HIPCHECK(launch_expert_gemm(GEMM_GATE_UP, nt, g, L->max_items, st));
+    HIPCHECK(launch_fwht_a8(L->Z, S, L->zq, L->zs, L->zsum, st));
+    // down: B rows are slot rows of Z'
+    g.off = L->d_off_d;
+    g.slot_token = nullptr;
+    g.xq = L->zq; g.xs = L->zs; g.xsum = L->zsum;
+    g.K = I; g.R = H; g.Z = nullptr; g.Y = L->Y;
+    HIPCHECK(launch_expert_gemm(GEMM_DOWN, nt, g, L->max_items, st));
+    HIPCHECK(launch_combine(L->Y, L->tok_slots, T, H, K + (d.has_shared ? 1 : 0), K + 1, out, st));
+    return LLMOE_OK;
+}
+
+int llmoe_layer_forward(llmoe_layer* L, const float* x, const float* logits, int T, float* out, llmoe_stream stream) {
+    if (int rc = check_layer(L)) return rc;
+    if (int rc = check_T(L, T)) return rc;
+    if (!x || !out) return fail(LLMOE_EINVAL, "null argument");
+    if (int rc = llmoe_quantize_a8(x, T, L->d.hidden, L->xq, L->xs, L->xsum, stream)) return rc;
+    if (int rc = llmoe_route(L, logits ? nullptr : x, logits, T, stream)) return rc;
+    return llmoe_experts(L, L->xq, L->xs, L->xsum, T, out, stream);
+}
+
+int llmoe_layer_buffers(const llmoe_layer* L, llmoe_buffers* o) {
+    if (int rc = check_layer(L)) return rc;
+    if (!o) return fail(LLMOE_EINVAL, "null argument");
+    o->xq = L->xq; o->xs = L->xs; o->xsum = L->xsum;
+    o->logits_part = L->part;
+    o->topk = L->topk; o->topw = L->topw;
+    o->count = L->count; o->start = L->start;
+    o->slot_token = L->slot_token; o->slot_weight = L->slot_weight; o->tok_slots = L->tok_slots;
+    o->items = reinterpret_cast<int32_t*>(L->items); o->n_items = L->n_items;
+    o->Z = L->Z; o->zq = L->zq; o->zs = L->zs; o->zsum = L->zsum; o->Y = L->Y;
+    o->ntok = L->ntok; o->max_items = L->max_items;
+    return LLMOE_OK;
+}
+
+int llmoe_layer_weight_bytes(const llmoe_layer* L, size_t* bytes) {
+    if (int rc = check_layer(L)) return rc;
+    if (!bytes) return fail(LLMOE_EINVAL, "null argument");
+    *bytes = L->weight_bytes;
+    return LLMOE_OK;
+}
+
+int llmoe_group_products(llmoe_layer* L, int expert, int which, const int8_t* xq, const int32_t* xsum, int n,
+                         int32_t* P, llmoe_stream stream) {
+    if (int rc = check_layer(L)) return rc;
+    if (!xq || !xsum || !P) return fail(LLMOE_EINVAL, "null argument");
+    if (expert < 0 || expert >= L->nexp) return fail(LLMOE_EINVAL, "expert %d", expert);
+    if (which != 0 && which != 1) return fail(LLMOE_EINVAL, "which = %d", which);
+    if (n < 1 || n > 64) return fail(LLMOE_EINVAL, "n = %d outside [1, 64]", n);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    L->p_item_host = Item{expert, 0, n, 0};
+    HIPCHECK(hipMemcpyAsync(L->p_item, &L->p_item_host, sizeof(Item), hipMemcpyHostToDevice, st));
+    HIPCHECK(hipMemcpyAsync(L->p_count, &L->p_count_host, sizeof(int), hipMemcpyHostToDevice, st));
+    GemmArgs g{};
+    g.base = L->arena;
+    g.off = which == 0 ? L->gu_off_d : L->d_off_d;
+    g.bits = L->bits_d;
+    g.items = L->p_item;
+    g.n_items = L->p_count;
+    g.xq = xq; g.xs = nullptr; g.xsum = xsum;
+    g.K = which == 0 ? L->d.hidden : L->d.inter;
+    g.R = which == 0 ? 2 * L->d.inter : L->d.hidden;
+    g.P = P;
+    HIPCHECK(launch_expert_gemm(which == 0 ? GEMM_PRODUCTS_GATE_UP : GEMM_PRODUCTS_DOWN, 4, g, 1, st));
+    HIPCHECK(hipStreamSynchronize(st));   // the host item record must outlive the copy
+    return LLMOE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,285 @@
+// Routed-expert W(2/3/4/8)·A8 GEMMs on gfx950 int8 MFMA (v_mfma_i32_16x16x64_i8).
+//
+// Math (engine/moe_i8.cu:1-14, :364-383): per 128-group g of the reduction
+//     P_g[r, n] = sum_{k in g} code[r, k] xq[n, k] - zero[r, g] Sxq[n, g]          (exact int32)
+//     acc[r, n] = fma(scale_w[r, g] * scale_x[n, g], float(P_g[r, n]), acc[r, n])  (fp32, g ascending)
+// The zero-point term enters as the MFMA's initial accumulator, so no integer work follows the MFMA.
+// 8-bit codes are stored as code - 128 (signed), and their zero as zero - 128 in the same product.
+//
+// Work decomposition (one work item = up to 16*NT slots of ONE expert, so the expert's weights stream from HBM
+// once per item): grid (row blocks, items); a workgroup = 4 waves; wave w owns SPW consecutive 16-row strips and
+// streams them through a register ring (dwordx4 loads, 1 KiB contiguous per wave and load). The item's B rows
+// (int8 activations + per-group scales and sums) are staged once per workgroup in LDS.
+//   gate_up (MODE 0): rows 2I = 1024, K = H = 2048, SPW 1; out Z[slot, i] = fp16(SiLU(g_i) u_i)
+//                     (engine/moe_i8.cu:219-221)
+//   down    (MODE 1): rows H = 2048, K = I = 512, SPW 4;  out Y[slot, h] = w_slot acc (engine/moe_i8.cu:222-231)
+//   products (MODE 2, 3): raw P_g per (token, row, group) in either geometry, for the bit-exactness test.
+#include "llmoe_internal.h"
+
+namespace llmoe {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+
+constexpr int WAVES = 4;
+
+template <int BITS>
+struct Step {               // one strip-superblock of one lane: codes + meta
+    u4 c[BITS];
+    u4 s0, s1;              // fp16 scales: s0 = tiles 0,1; s1 = tiles 2,3 (4 rows each)
+    u4 z;                   // u8 zeros: word tau = rows 0..3 of tile tau
+};
+
+template <int BITS>
+__device__ __forceinline__ void load_step(const uint8_t* sbp, int lane, Step<BITS>& r) {
+    const int q = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < BITS; ++i) r.c[i] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(sbp + i * 1024) + lane);
+    const uint8_t* meta = sbp + BITS * 1024;
+    r.s0 = *reinterpret_cast<const u4*>(meta + 32 * q);
+    r.s1 = *reinterpret_cast<const u4*>(meta + 32 * q + 16);
+    r.z = *reinterpret_cast<const u4*>(meta + 128 + 16 * q);
+}
+
+__device__ __forceinline__ uint32_t wsel(const u4& v, int i) { return v[i]; }
+
+// The 8 A-operand dwords of tile tau: D[0..3] feed the MFMA of columns 0..63, D[4..7] columns 64..127.
+template <int BITS>
+__device__ __forceinline__ void unpack_tile(const Step<BITS>& r, int tau, uint32_t (&D)[8]) {
+    if constexpr (BITS == 2 || BITS == 3) {
+        const u4& u = r.c[tau >> 1];
+        const uint32_t p0 = (tau & 1) ? u.z : u.x, p1 = (tau & 1) ? u.w : u.y;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            D[s] = (p0 >> (2 * s)) & 0x03030303u;
+            D[4 + s] = (p1 >> (2 * s)) & 0x03030303u;
+        }
+        if constexpr (BITS == 3) {
+            const uint32_t h = wsel(r.c[2], tau);
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const uint32_t hb = s >= 2 ? (h >> (s - 2)) : (h << (2 - s));
+                D[s] |= hb & 0x04040404u;
+            }
+        }
+    } else if constexpr (BITS == 4) {
+        const u4& u = r.c[tau];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t w = wsel(u, m);
+            D[2 * m] = w & 0x0F0F0F0Fu;
+            D[2 * m + 1] = (w >> 4) & 0x0F0F0F0Fu;
+        }
+    } else {
+        const u4& a = r.c[2 * tau];
+        const u4& b = r.c[2 * tau + 1];
+        D[0] = a.x; D[1] = a.y; D[2] = a.z; D[3] = a.w;
+        D[4] = b.x; D[5] = b.y; D[6] = b.z; D[7] = b.w;
+    }
+}
+
+// packlib strip row of device gate_up strip row d (inverse of the interleave written by relayout.hip)
+__device__ __forceinline__ int gu_packlib_row(int d) {
+    const int q = d >> 2, v = d & 3;
+    return (v & 1) ? 8 + 2 * q + (v >> 1) : 2 * q + (v >> 1);
+}
+
+template <int MODE>
+struct Geo {
+    static constexpr bool DOWN_SHAPE = MODE == GEMM_DOWN || MODE == GEMM_PRODUCTS_DOWN;
+    static constexpr bool PRODUCTS = MODE == GEMM_PRODUCTS_GATE_UP || MODE == GEMM_PRODUCTS_DOWN;
+    static constexpr int NSB = DOWN_SHAPE ? 1 : 4;       // K = 512 or 2048
+    static constexpr int SPW = DOWN_SHAPE ? 4 : 1;
+};
+
+template <int BITS>
+struct Ring {
+    static constexpr int D = BITS <= 3 ? 4 : BITS == 4 ? 3 : 2;
+};
+
+__host__ __device__ constexpr int lds_bytes(int ntok, int K) { return ntok * (K + 16) + ntok * (K / GROUP) * 8; }
+
+template <int BITS, int MODE, int NT>
+__device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uint8_t* lds, int row_block) {
+    constexpr int NSB = Geo<MODE>::NSB, SPW = Geo<MODE>::SPW, NSTEP = NSB * SPW, D = Ring<BITS>::D;
+    constexpr int K = NSB * SB_K, G = K / GROUP, NTOK = 16 * NT, LDQ = K + 16;
+    constexpr size_t SBB = sb_bytes(BITS);
+    constexpr int ZOFF = BITS == 8 ? 128 : 0;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, col = lane & 15;
+    const int strip0 = (row_block * WAVES + wave) * SPW;
+    const uint8_t* mat = a.base + a.off[it.expert] + size_t(strip0) * NSB * SBB;
+
+    // weight prefetch first: its latency overlaps the B staging below
+    Step<BITS> ring[D];
+#pragma unroll
+    for (int u = 0; u < D; ++u)
+        if (u < NSTEP) load_step<BITS>(mat + size_t(u) * SBB, lane, ring[u]);
+
+    // stage the item's B rows in LDS: q8 rows [NTOK][LDQ], scales [G][NTOK], sums [G][NTOK]
+    int8_t* bq = reinterpret_cast<int8_t*>(lds);
+    float* bs = reinterpret_cast<float*>(lds + NTOK * LDQ);
+    int* bsum = reinterpret_cast<int*>(bs + G * NTOK);
+    const int ntok = it.ntok;
+    for (int v = threadIdx.x; v < ntok * (K / 16); v += WAVES * 64) {
+        const int n = v / (K / 16), c16 = v % (K / 16);
+        const int slot = it.slot0 + n;
+        const size_t row = a.slot_token ? size_t(a.slot_token[slot]) : size_t(slot);
+        *reinterpret_cast<uint4*>(bq + n * LDQ + 16 * c16) = *reinterpret_cast<const uint4*>(a.xq + row * K + 16 * c16);
+    }
+    for (int v = threadIdx.x; v < ntok * G; v += WAVES * 64) {
+        const int n = v / G, g = v % G;
+        const int slot = it.slot0 + n;
+        const size_t row = a.slot_token ? size_t(a.slot_token[slot]) : size_t(slot);
+        bs[g * NTOK + n] = a.xs ? a.xs[row * G + g] : 0.0f;
+        bsum[g * NTOK + n] = a.xsum[row * G + g];
+    }
+    __syncthreads();
+
+    float acc[NT][4];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt][0] = acc[nt][1] = acc[nt][2] = acc[nt][3] = 0.0f;
+
+#pragma unroll
+    for (int u = 0; u < NSTEP; ++u) {
+        const Step<BITS> cur = ring[u % D];
+        if (u + D < NSTEP) load_step<BITS>(mat + size_t(u + D) * SBB, lane, ring[u % D]);
+        const int sb = u % NSB, strip = strip0 + u / NSB;
+#pragma unroll
+        for (int tau = 0; tau < 4; ++tau) {
+            const int g = sb * 4 + tau;
+            uint32_t Dw[8];
+            unpack_tile<BITS>(cur, tau, Dw);
+            const v4i A0 = {int(Dw[0]), int(Dw[1]), int(Dw[2]), int(Dw[3])};
+            const v4i A1 = {int(Dw[4]), int(Dw[5]), int(Dw[6]), int(Dw[7])};
+            const uint32_t zw = wsel(cur.z, tau);
+            const u4& sv = tau < 2 ? cur.s0 : cur.s1;
+            const uint32_t s01 = wsel(sv, (tau & 1) * 2), s23 = wsel(sv, (tau & 1) * 2 + 1);
+            float sw[4];
+            sw[0] = f16_bits_to_f32(s01 & 0xFFFFu);
+            sw[1] = f16_bits_to_f32(s01 >> 16);
+            sw[2] = f16_bits_to_f32(s23 & 0xFFFFu);
+            sw[3] = f16_bits_to_f32(s23 >> 16);
+            int zz[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) zz[v] = int((zw >> (8 * v)) & 0xFFu) - ZOFF;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int n = nt * 16 + col;
+                v4i B0 = {0, 0, 0, 0}, B1 = {0, 0, 0, 0};
+                float xsn = 0.0f;
+                int xsumn = 0;
+                if (n < ntok) {
+                    const int8_t* br = bq + n * LDQ + g * GROUP + 16 * q;
+                    B0 = *reinterpret_cast<const v4i*>(br);
+                    B1 = *reinterpret_cast<const v4i*>(br + 64);
+                    xsn = bs[g * NTOK + n];
+                    xsumn = bsum[g * NTOK + n];
+                }
+                v4i C = {-__mul24(zz[0], xsumn), -__mul24(zz[1], xsumn), -__mul24(zz[2], xsumn), -__mul24(zz[3], xsumn)};
+                C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, C, 0, 0, 0);
+                C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, C, 0, 0, 0);
+                if constexpr (Geo<MODE>::PRODUCTS) {
+                    if (n < ntok) {
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            const int d = 4 * q + v;
+                            const int prow = 16 * strip + (MODE == GEMM_PRODUCTS_GATE_UP ? gu_packlib_row(d) : d);
+                            a.P[(size_t(it.slot0 + n) * a.R + prow) * G + g] = C[v];
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[nt][v] = __builtin_fmaf(sw[v] * xsn, float(C[v]), acc[nt][v]);
+                }
+            }
+        }
+        if constexpr (!Geo<MODE>::PRODUCTS) {
+            if (sb == NSB - 1) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const int n = nt * 16 + col;
+                    if (n < ntok) {
+                        const int slot = it.slot0 + n;
+                        if constexpr (MODE == GEMM_GATE_UP) {
+                            // lane quad q holds rows gate 8 strip + 2q, up (same), gate + 1, up + 1
+                            const uint32_t z0 = f32_to_f16_bits(silu_f32(acc[nt][0]) * acc[nt][1]);
+                            const uint32_t z1 = f32_to_f16_bits(silu_f32(acc[nt][2]) * acc[nt][3]);
+                            *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
+                        } else {
+                            const float w = a.slot_weight[slot];
+                            *reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q) =
+                                make_float4(w * acc[nt][0], w * acc[nt][1], w * acc[nt][2], w * acc[nt][3]);
+                        }
+                    }
+                    acc[nt][0] = acc[nt][1] = acc[nt][2] = acc[nt][3] = 0.0f;
+                }
+            }
+        }
+    }
+}
+
+template <int MODE, int NT>
+__global__ void __launch_bounds__(WAVES * 64) expert_gemm(GemmArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int item = blockIdx.y;
+    if (item >= *a.n_items) return;
+    const Item it = a.items[item];
+    const int bits = a.bits[it.expert];
+    if (bits == 2) gemm_body<2, MODE, NT>(a, it, lds, blockIdx.x);
+    else if (bits == 3) gemm_body<3, MODE, NT>(a, it, lds, blockIdx.x);
+    else if (bits == 4) gemm_body<4, MODE, NT>(a, it, lds, blockIdx.x);
+    else gemm_body<8, MODE, NT>(a, it, lds, blockIdx.x);
+}
+
+template <int MODE, int NT>
+const void* kernel_ptr() { return reinterpret_cast<const void*>(&expert_gemm<MODE, NT>); }
+
+template <int MODE, int NT>
+hipError_t set_attr() {
+    constexpr int K = Geo<MODE>::NSB * SB_K;
+    return hipFuncSetAttribute(kernel_ptr<MODE, NT>(), hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes(16 * NT, K));
+}
+
+template <int MODE, int NT>
+hipError_t launch_t(const GemmArgs& a, int max_items, hipStream_t st) {
+    constexpr int K = Geo<MODE>::NSB * SB_K;
+    const int rows_per_block = 16 * WAVES * Geo<MODE>::SPW;
+    const dim3 grid(a.R / rows_per_block, max_items);
+    expert_gemm<MODE, NT><<<grid, WAVES * 64, lds_bytes(16 * NT, K), st>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t gemm_setup() {
+    hipError_t e;
+    if ((e = set_attr<GEMM_GATE_UP, 1>()) != hipSuccess) return e;
+    if ((e = set_attr<GEMM_GATE_UP, 2>()) != hipSuccess) return e;
+    if ((e = set_attr<GEMM_GATE_UP, 4>()) != hipSuccess) return e;
+    if ((e = set_attr<GEMM_DOWN, 1>()) != hipSuccess) return e;
+    if ((e = set_attr<GEMM_DOWN, 2>()) != hipSuccess) return e;
+    if ((e = set_attr<GEMM_DOWN, 4>()) != hipSuccess) return e;
+    if ((e = set_attr<GEMM_PRODUCTS_GATE_UP, 4>()) != hipSuccess) return e;
+    if ((e = set_attr<GEMM_PRODUCTS_DOWN, 4>()) != hipSuccess) return e;
+    return hipSuccess;
+}
+
+// mode: GemmMode; nt: 1, 2 or 4 (16-token tiles per item; the products modes always run NT = 4).
+hipError_t launch_expert_gemm(int mode, int nt, const GemmArgs& a, int max_items, hipStream_t st) {
+    if (mode == GEMM_GATE_UP) {
+        if (nt == 1) return launch_t<GEMM_GATE_UP, 1>(a, max_items, st);
+        if (nt == 2) return launch_t<GEMM_GATE_UP, 2>(a, max_items, st);
+        return launch_t<GEMM_GATE_UP, 4>(a, max_items, st);
+    }
+    if (mode == GEMM_DOWN) {
+        if (nt == 1) return launch_t<GEMM_DOWN, 1>(a, max_items, st);
+        if (nt == 2) return launch_t<GEMM_DOWN, 2>(a, max_items, st);
+        return launch_t<GEMM_DOWN, 4>(a, max_items, st);
+    }
+    if (mode == GEMM_PRODUCTS_GATE_UP) return launch_t<GEMM_PRODUCTS_GATE_UP, 4>(a, max_items, st);
+    return launch_t<GEMM_PRODUCTS_DOWN, 4>(a, max_items, st);
+}
+
+}  // namespace llmoe

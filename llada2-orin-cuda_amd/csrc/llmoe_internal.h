@@ -1,0 +1,128 @@
+// Internal declarations shared by the libllmoe translation units: device data formats, numeric helpers that
+// must match the CPU checker bit for bit, and the host-side launchers each kernel file exports.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+
+namespace llmoe {
+
+constexpr int GROUP = 128;       // quantisation group along K (weights and activations)
+constexpr int SB_K = 512;        // K columns per superblock = 4 groups
+constexpr int META_SB = 192;     // per strip and superblock: 64 fp16 scales + 64 u8 zeros
+constexpr int ROUTER_KC = 8;     // router K chunks (fixed summation order)
+
+// One work item of the expert GEMMs: `ntok` consecutive slots of one expert.
+struct Item {
+    int expert;
+    int slot0;
+    int ntok;
+    int pad;
+};
+
+// Device weight layout (written by relayout_matrix from packlib "i8"):
+//   matrix [R, K] = R/16 strips of 16 rows; a strip = K/512 superblocks; a superblock (4 groups of 128) =
+//     BITS x 1024 B of codes: load i of lane l (64 lanes) at i*1024 + 16 l (one dwordx4 per lane and load)
+//     128 B scales  [q 4][tile 4][v 4] fp16      (lane quad q = l/16 reads 32 B at 32 q)
+//      64 B zeros   [q 4][tile 4][v 4] u8        (lane quad q reads 16 B at 128 + 16 q)
+//   so one superblock has the same byte count as 4 packlib tiles (4 (256 BITS + 48)).
+// Lane l of the MFMA A operand holds strip row l%16 and, for the group's two 64-column halves h, columns
+//   64 h + 16 (l/16) + 0..15; output row 4 (l/16) + v of v_mfma_i32_16x16x64_i8 is strip row 4 (l/16) + v.
+// gate_up strips are stored in the row order gate j, up j, gate j+1, up j+1 per lane quad, so each lane ends
+// with the gate and up accumulators of the same intermediate channels (see relayout.hip).
+__host__ __device__ constexpr size_t sb_bytes(int bits) { return size_t(bits) * 1024 + META_SB; }
+__host__ __device__ constexpr size_t matrix_dev_bytes(int R, int K, int bits) {
+    return size_t(R / 16) * size_t(K / SB_K) * sb_bytes(bits);
+}
+
+// ---- numerics shared with the CPU checker (same fp32 operation sequence, compiled with fp-contract off) ----
+
+__device__ __forceinline__ float pow2i(int k) { return __int_as_float((k + 127) << 23); }
+
+// exp(x): Cody-Waite reduction with ln2 = hi + lo (hi has 12 trailing zero bits), Taylor polynomial of degree 7
+// on |r| <= ln2/2, scaling by 2^n as two exact power-of-two factors.
+__device__ __forceinline__ float exp_f32(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_inff();
+    if (x < -103.97208404541016f) return 0.0f;
+    const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+    float r = __builtin_fmaf(n, -0.693145751953125f, x);
+    r = __builtin_fmaf(n, -1.428606765330187045037746429443359375e-06f, r);
+    float p = 1.98412701138295233249664306640625e-04f;
+    p = __builtin_fmaf(p, r, 1.38888892345130443572998046875e-03f);
+    p = __builtin_fmaf(p, r, 8.33333376795053482055664062500e-03f);
+    p = __builtin_fmaf(p, r, 4.16666679084300994873046875000e-02f);
+    p = __builtin_fmaf(p, r, 1.66666671633720397949218750000e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int ni = int(n), e1 = ni / 2, e2 = ni - e1;
+    return (p * pow2i(e1)) * pow2i(e2);
+}
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + exp_f32(-x)); }
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + exp_f32(-x)); }
+
+// fp32 -> fp16 with round-to-nearest-even on exact ties, in integer ops. (Measured on gfx950: v_cvt_f16_f32
+// does not round every exact halfway case to even, so the hardware conversion is not used.)
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+    uint32_t h;
+    if (ax >= 0x7f800000u) {
+        h = 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u);              // inf / nan
+    } else if (ax >= 0x477ff000u) {
+        h = 0x7c00u;                                                  // >= 65520 rounds to inf
+    } else if (ax < 0x38800000u) {
+        h = uint32_t(__builtin_rintf(__uint_as_float(ax) * 16777216.0f));   // subnormal half: exact scale by 2^24
+    } else {
+        const uint32_t mant = ax & 0x7fffffu;
+        h = ((((ax >> 23) - 112u)) << 10) | (mant >> 13);
+        const uint32_t rem = mant & 0x1fffu;
+        h += (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ? 1u : 0u;
+    }
+    return uint16_t(sign | h);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+
+// ---- host launchers (each returns the launch's hipError_t) ----
+
+struct GemmArgs {
+    const uint8_t* base;        // device weight arena
+    const uint64_t* off;        // [E+1] byte offset of the matrix of each expert (gate_up or down)
+    const int8_t* bits;         // [E+1]
+    const Item* items;
+    const int* n_items;         // device count; blocks with item >= *n_items exit
+    const int* slot_token;      // gate_up: B row of slot s is token slot_token[s]; nullptr: row = slot
+    const int8_t* xq;           // B rows, int8 [rows, K]
+    const float* xs;            // [rows, K/128]
+    const int* xsum;            // [rows, K/128]
+    const float* slot_weight;   // down: Y = w_slot * acc
+    int K;                      // reduction length (H for gate_up, I for down)
+    int R;                      // output rows (2I for gate_up, H for down)
+    uint16_t* Z;                // gate_up out [slots, R/2] fp16
+    float* Y;                   // down out [slots, R]
+    int32_t* P;                 // group-products out [n, R, K/128] (test entry)
+};
+
+enum GemmMode { GEMM_GATE_UP = 0, GEMM_DOWN = 1, GEMM_PRODUCTS_GATE_UP = 2, GEMM_PRODUCTS_DOWN = 3 };
+
+hipError_t gemm_setup();   // function attributes (dynamic LDS), once per process
+hipError_t launch_expert_gemm(int mode, int nt, const GemmArgs& a, int max_items, hipStream_t st);
+hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, int R, int K, int bits, int gate_up, hipStream_t st);
+hipError_t launch_quant_a8(const float* x, int rows, int cols, int8_t* q, float* s, int* sum, hipStream_t st);
+hipError_t launch_fwht_a8(const uint16_t* Z, int nslots, int8_t* q, float* s, int* sum, hipStream_t st);
+hipError_t launch_combine(const float* Y, const int* tok_slots, int T, int H, int kk, int K1, float* out,
+                          hipStream_t st);
+hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, int E, float* part, hipStream_t st);
+hipError_t launch_route(const float* part, int nchunks, const float* bias, int T, int E, int K, int C, int block,
+                        float rscale, int32_t* topk, float* topw, uint32_t* mask, hipStream_t st);
+hipError_t launch_masks(const int32_t* topk, int T, int E, int K, int block, uint32_t* mask, hipStream_t st);
+hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int has_shared, int ntok,
+                       int32_t* count, int32_t* start, int32_t* bpre, Item* items, int* n_items, hipStream_t st);
+hipError_t launch_place(const int32_t* topk, const float* topw, const uint32_t* mask, const int32_t* bpre, int T,
+                        int E, int K, int block, int has_shared, int32_t* slot_token, float* slot_weight,
+                        int32_t* tok_slots, hipStream_t st);
+
+}  // namespace llmoe

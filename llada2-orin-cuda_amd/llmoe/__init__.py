@@ -1,0 +1,219 @@
+"""Python binding of libllmoe (include/llmoe.h): the LLaDA2 routed-expert MoE layer on MI355X.
+
+The compute path is the HIP library libllmoe.so next to this file (built by `python -m llmoe.build` or
+`__graft_entry__.build()`); this module only marshals arguments. There is no fallback: if the library is not
+built, loading fails loudly.
+
+Device memory and streams come from PyTorch (torch.cuda tensors and torch.cuda.current_stream()); every call
+passes raw device pointers through the C ABI, as the reference's server binds its engine through ctypes
+(server/server.py:62-71 of patrickbdevaney/llada2-orin-cuda).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = _HERE / "libllmoe.so"
+
+LLMOE_OK = 0
+
+
+class LLMoEError(RuntimeError):
+    pass
+
+
+class LayerDesc(ctypes.Structure):
+    _fields_ = [
+        ("hidden", ctypes.c_int),
+        ("inter", ctypes.c_int),
+        ("n_experts", ctypes.c_int),
+        ("top_k", ctypes.c_int),
+        ("pool", ctypes.c_int),
+        ("block", ctypes.c_int),
+        ("routed_scale", ctypes.c_float),
+        ("has_shared", ctypes.c_int),
+        ("max_tokens", ctypes.c_int),
+    ]
+
+
+class Buffers(ctypes.Structure):
+    _fields_ = [
+        ("xq", ctypes.c_void_p), ("xs", ctypes.c_void_p), ("xsum", ctypes.c_void_p),
+        ("logits_part", ctypes.c_void_p),
+        ("topk", ctypes.c_void_p), ("topw", ctypes.c_void_p),
+        ("count", ctypes.c_void_p), ("start", ctypes.c_void_p),
+        ("slot_token", ctypes.c_void_p), ("slot_weight", ctypes.c_void_p),
+        ("tok_slots", ctypes.c_void_p),
+        ("items", ctypes.c_void_p), ("n_items", ctypes.c_void_p),
+        ("Z", ctypes.c_void_p), ("zq", ctypes.c_void_p), ("zs", ctypes.c_void_p), ("zsum", ctypes.c_void_p),
+        ("Y", ctypes.c_void_p),
+        ("ntok", ctypes.c_int), ("max_items", ctypes.c_int),
+    ]
+
+
+EXPORTS = [
+    "llmoe_layer_create", "llmoe_layer_destroy", "llmoe_quantize_a8", "llmoe_route", "llmoe_dispatch",
+    "llmoe_experts", "llmoe_layer_forward", "llmoe_layer_buffers", "llmoe_layer_weight_bytes",
+    "llmoe_group_products", "llmoe_last_error",
+]
+
+_lib = None
+
+
+def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
+    """Load libllmoe.so (raises if it is not built: the HIP path is the only path)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise LLMoEError(f"{p} is not built; run __graft_entry__.build() (hipcc --offload-arch=gfx950)")
+    lib = ctypes.CDLL(str(p))
+    vp, i, f, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    lib.llmoe_last_error.restype = ctypes.c_char_p
+    lib.llmoe_layer_create.argtypes = [ctypes.POINTER(LayerDesc), vp, sz, vp, vp, vp, vp, vp,
+                                       ctypes.POINTER(ctypes.c_void_p)]
+    lib.llmoe_layer_destroy.argtypes = [vp]
+    lib.llmoe_quantize_a8.argtypes = [vp, i, i, vp, vp, vp, vp]
+    lib.llmoe_route.argtypes = [vp, vp, vp, i, vp]
+    lib.llmoe_dispatch.argtypes = [vp, vp, vp, i, vp]
+    lib.llmoe_experts.argtypes = [vp, vp, vp, vp, i, vp, vp]
+    lib.llmoe_layer_forward.argtypes = [vp, vp, vp, i, vp, vp]
+    lib.llmoe_layer_buffers.argtypes = [vp, ctypes.POINTER(Buffers)]
+    lib.llmoe_layer_weight_bytes.argtypes = [vp, ctypes.POINTER(sz)]
+    lib.llmoe_group_products.argtypes = [vp, i, i, vp, vp, i, vp, vp]
+    for name in EXPORTS:
+        if name != "llmoe_last_error":
+            getattr(lib, name).restype = ctypes.c_int
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _check(rc: int) -> None:
+    if rc != LLMOE_OK:
+        msg = load_library().llmoe_last_error().decode(errors="replace")
+        raise LLMoEError(f"libllmoe error {rc}: {msg}")
+
+
+def _ptr(t) -> int | None:
+    """Device (or host numpy) pointer of a tensor / array, None for None."""
+    if t is None:
+        return None
+    if isinstance(t, np.ndarray):
+        assert t.flags["C_CONTIGUOUS"]
+        return t.ctypes.data
+    assert t.is_contiguous(), "tensors passed to libllmoe must be contiguous"
+    return t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else stream
+
+
+class Layer:
+    """One MoE layer resident in HBM (llmoe_layer_*). Weights: packlib format "i8" blob + per-expert tables."""
+
+    def __init__(self, blob: np.ndarray, gu_off, d_off, bits, router_bias, router_w=None, *, hidden=2048, inter=512,
+                 n_experts=256, top_k=8, pool=256, block=32, routed_scale=2.5, has_shared=False, max_tokens=4096):
+        self.lib = load_library()
+        self.desc = LayerDesc(hidden, inter, n_experts, top_k, pool, block, routed_scale, int(has_shared), max_tokens)
+        blob = np.ascontiguousarray(blob, dtype=np.uint8)
+        gu_off = np.ascontiguousarray(gu_off, dtype=np.uint64)
+        d_off = np.ascontiguousarray(d_off, dtype=np.uint64)
+        bits = np.ascontiguousarray(bits, dtype=np.int8)
+        bias = np.ascontiguousarray(router_bias, dtype=np.float32)
+        rw = None if router_w is None else np.ascontiguousarray(router_w, dtype=np.float32)
+        h = ctypes.c_void_p()
+        _check(self.lib.llmoe_layer_create(ctypes.byref(self.desc), _ptr(blob), blob.nbytes, _ptr(gu_off),
+                                           _ptr(d_off), _ptr(bits), _ptr(rw), _ptr(bias), ctypes.byref(h)))
+        self.handle = h
+        self.T = None
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            _check(self.lib.llmoe_layer_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- calls (device tensors in, device tensors out) ----
+    def forward(self, x, logits=None, out=None, stream=None):
+        import torch
+        T = x.shape[0]
+        if out is None:
+            out = torch.empty((T, self.desc.hidden), dtype=torch.float32, device=x.device)
+        _check(self.lib.llmoe_layer_forward(self.handle, _ptr(x), _ptr(logits), T, _ptr(out), _stream(stream)))
+        self.T = T
+        return out
+
+    def route(self, T, x=None, logits=None, stream=None):
+        _check(self.lib.llmoe_route(self.handle, _ptr(x), _ptr(logits), T, _stream(stream)))
+        self.T = T
+
+    def dispatch(self, topk, topw, stream=None):
+        T = topk.shape[0]
+        _check(self.lib.llmoe_dispatch(self.handle, _ptr(topk), _ptr(topw), T, _stream(stream)))
+        self.T = T
+
+    def experts(self, xq, xs, xsum, out=None, stream=None):
+        import torch
+        T = xq.shape[0]
+        if out is None:
+            out = torch.empty((T, self.desc.hidden), dtype=torch.float32, device=xq.device)
+        _check(self.lib.llmoe_experts(self.handle, _ptr(xq), _ptr(xs), _ptr(xsum), T, _ptr(out), _stream(stream)))
+        return out
+
+    def group_products(self, expert: int, which: int, xq, xsum, stream=None):
+        import torch
+        n, kw = xq.shape
+        rows = 2 * self.desc.inter if which == 0 else self.desc.hidden
+        P = torch.zeros((n, rows, kw // 128), dtype=torch.int32, device=xq.device)
+        _check(self.lib.llmoe_group_products(self.handle, expert, which, _ptr(xq), _ptr(xsum), n, _ptr(P),
+                                             _stream(stream)))
+        return P
+
+    def buffers(self) -> Buffers:
+        b = Buffers()
+        _check(self.lib.llmoe_layer_buffers(self.handle, ctypes.byref(b)))
+        return b
+
+    def weight_bytes(self) -> int:
+        v = ctypes.c_size_t()
+        _check(self.lib.llmoe_layer_weight_bytes(self.handle, ctypes.byref(v)))
+        return int(v.value)
+
+    def read(self, name: str, shape, dtype):
+        """Copy a workspace buffer (llmoe_buffers field) to a numpy array (synchronises the device)."""
+        import torch
+        ptr = getattr(self.buffers(), name)
+        n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        torch.cuda.synchronize()
+        out = np.empty(shape, dtype=dtype)
+        _hip_memcpy_d2h(out, ptr, n)
+        return out
+
+
+_hip = None
+
+
+def _hip_memcpy_d2h(dst: np.ndarray, src_ptr: int, nbytes: int) -> None:
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+        _hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        _hip.hipMemcpy.restype = ctypes.c_int
+    rc = _hip.hipMemcpy(dst.ctypes.data, src_ptr, nbytes, 2)   # hipMemcpyDeviceToHost
+    if rc != 0:
+        raise LLMoEError(f"hipMemcpy D2H failed: {rc}")

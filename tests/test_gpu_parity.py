@@ -1,0 +1,214 @@
+"""GPU parity: libllmoe.so (HIP, gfx950) against the CPU oracle on the same seeded inputs.
+
+The bar: integer outputs (A8 codes and sums, expert indices, slots, work items, int32 group products) bit-exact;
+fp32 outputs (router logits, routing weights, SiLU -> fp16, FWHT + A8 scales, expert outputs, combine) bit-exact
+as well, since both sides run the same fp32 operation sequence -- and, as the contract's floor, within max-abs
+1e-3 relative (FP_TOL) of the oracle.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from llmoe import Layer, synth
+
+pytestmark = pytest.mark.gpu
+
+FP_TOL = 1e-3   # max |gpu - oracle| <= FP_TOL * max |oracle|
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def close(gpu, ref, what):
+    gpu = np.asarray(gpu, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(gpu - ref).max() if gpu.size else 0.0
+    scale = max(np.abs(ref).max() if ref.size else 0.0, 1e-30)
+    assert err <= FP_TOL * scale, f"{what}: max abs err {err} > {FP_TOL} * {scale}"
+
+
+def make_gpu_layer(L, pool, max_tokens=256, K=8):
+    return Layer(L["blob"], L["gu_off"], L["d_off"], L["bits"], L["bias"], L["Wr"], n_experts=L["E"], top_k=K,
+                 pool=pool, has_shared=L["shared"], max_tokens=max_tokens)
+
+
+_LAYERS = {}
+
+
+def layer_for(mix, shared, seed=11):
+    key = (mix, shared, seed)
+    if key not in _LAYERS:
+        _LAYERS[key] = synth.make_layer(seed, mix=mix, shared=shared)
+    return _LAYERS[key]
+
+
+# ------------------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("rows", [1, 7, 64])
+def test_quant_a8_bit_exact(gpu, rows):
+    import torch
+    import llmoe
+    say(f"[quant_a8] rows={rows}")
+    x = synth.make_x(100 + rows, rows, 2048, outlier_frac=0.01)
+    x[0, :128] = 0.0                       # an all-zero group: scale floor 1e-30
+    q_ref, s_ref, sum_ref = oracle.quant_a8(x)
+    xd = to_dev(x, gpu)
+    q = torch.empty((rows, 2048), dtype=torch.int8, device=gpu)
+    s = torch.empty((rows, 16), dtype=torch.float32, device=gpu)
+    sm = torch.empty((rows, 16), dtype=torch.int32, device=gpu)
+    lib = llmoe.load_library()
+    rc = lib.llmoe_quantize_a8(xd.data_ptr(), rows, 2048, q.data_ptr(), s.data_ptr(), sm.data_ptr(),
+                               torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(sm.cpu().numpy(), sum_ref)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("which", [0, 1])
+def test_group_products_bit_exact(gpu, bits, which):
+    """Exact int32 P_g = sum code*xq - zero*Sxq for every (token, row, group), through relayout + MFMA."""
+    say(f"[group_products] bits={bits} which={which}")
+    L = synth.make_layer(31 + bits, mix=bits, experts=[5])
+    G = make_gpu_layer(L, 256)
+    e = 5
+    R, Kw = (1024, 2048) if which == 0 else (2048, 512)
+    off = int(L["gu_off"][e] if which == 0 else L["d_off"][e])
+    codes, scale, zero = oracle.unpack_i8(L["blob"][off:off + synth.matrix_bytes(R, Kw, bits)], R, Kw, bits)
+    rng = np.random.default_rng(7)
+    n = 37
+    xq = rng.integers(-127, 128, (n, Kw), dtype=np.int8)
+    xq[0] = 127
+    xq[1] = -127
+    xsum = xq.reshape(n, -1, 128).astype(np.int32).sum(-1).astype(np.int32)
+    P = G.group_products(e, which, to_dev(xq, gpu), to_dev(xsum, gpu)).cpu().numpy()
+    for i in range(n):
+        ref = oracle.group_products(codes, zero, xq[i], xsum[i])
+        assert np.array_equal(P[i], ref), f"token {i}: {np.argwhere(P[i] != ref)[:5]}"
+    G.close()
+
+
+def run_layer(G, x, dev, logits=None):
+    import torch
+    out = G.forward(to_dev(x, dev), None if logits is None else to_dev(logits, dev))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def check_full(G, r, T, K, shared, tokens=None):
+    """Compare every stage of the GPU workspace with the oracle run r (optionally only some tokens)."""
+    H, I = 2048, 512
+    S = T * K + (T if shared else 0)
+    topk = G.read("topk", (T, K), np.int32)
+    topw = G.read("topw", (T, K), np.float32)
+    assert np.array_equal(topk, r["topk"]), "expert indices differ"
+    assert np.array_equal(topw.view(np.uint32), r["topw"].view(np.uint32)), "routing weights differ"
+    assert np.array_equal(G.read("slot_token", (S,), np.int32), r["slot_token"])
+    assert np.array_equal(G.read("slot_weight", (S,), np.float32), r["slot_weight"])
+    ts = G.read("tok_slots", (T, K + 1), np.int32)
+    assert np.array_equal(ts, r["tok_slots"])
+    E = r["count"].size
+    assert np.array_equal(G.read("count", (E,), np.int32), r["count"])
+    Z = G.read("Z", (S, I), np.uint16)
+    zq = G.read("zq", (S, I), np.int8)
+    zs = G.read("zs", (S, 4), np.float32)
+    zsum = G.read("zsum", (S, 4), np.int32)
+    Y = G.read("Y", (S, H), np.float32)
+    if tokens is None:
+        slots = np.arange(S)
+    else:
+        slots = np.unique(ts[tokens][:, :K + (1 if shared else 0)].reshape(-1))
+    for name, a, b in (("Z", Z, r["Z"]), ("zq", zq, r["zq"]), ("zsum", zsum, r["zsum"])):
+        assert np.array_equal(a[slots], b[slots]), f"{name} differs at slots {np.argwhere((a[slots] != b[slots]).any(-1))[:5].ravel()}"
+    close(zs[slots], r["zs"][slots], "zs")
+    assert np.array_equal(zs[slots].view(np.uint32), r["zs"][slots].view(np.uint32)), "zs not bit-exact"
+    close(Y[slots], r["Y"][slots], "Y")
+    assert np.array_equal(Y[slots].view(np.uint32), r["Y"][slots].view(np.uint32)), "Y not bit-exact"
+
+
+@pytest.mark.parametrize("T,mix,shared,pool", [
+    (32, 4, False, 48),          # config 0: 4-bit, block pool 48
+    (32, 4, False, 256),         # config 0 without the pool
+    (32, "mixed", True, 256),    # config 1
+    (1, "mixed", True, 256),
+    (45, "mixed", True, 48),     # ragged last block
+    (96, 8, True, 256),
+    (200, "mixed", True, 48),    # NT = 2 / 4 items
+])
+def test_layer_forward_matches_oracle(gpu, T, mix, shared, pool):
+    say(f"[layer] T={T} mix={mix} shared={shared} pool={pool}")
+    L = layer_for(mix, shared)
+    G = make_gpu_layer(L, pool)
+    x = synth.make_x(1000 + T, T)
+    out = run_layer(G, x, gpu)
+    r = oracle.Layer(L).forward(x, C=pool)
+    assert np.array_equal(G.read("xq", (T, 2048), np.int8), r["xq"])
+    check_full(G, r, T, 8, shared)
+    close(out, r["out"], "out")
+    assert np.array_equal(out.view(np.uint32), r["out"].view(np.uint32)), "combine not bit-exact"
+    ref64 = oracle.Layer(L).reference_f64(x, r["topk"], r["topw"])
+    assert np.linalg.norm(out - ref64) / np.linalg.norm(ref64) < 5e-3   # engine/tests/test_moe_i8.cu:173
+    G.close()
+
+
+@pytest.mark.parametrize("kind", ["zipf", "skewed"])
+def test_logits_routing(gpu, kind):
+    T = 128
+    say(f"[logits routing] {kind} T={T}")
+    L = synth.make_layer(21, mix="mixed", shared=True, zero_bias=True)
+    lg = synth.logits_zipf(5, T) if kind == "zipf" else synth.logits_skewed(5, T)
+    G = make_gpu_layer(L, 256)
+    x = synth.make_x(77, T)
+    out = run_layer(G, x, gpu, logits=lg)
+    r = oracle.Layer(L).forward(x, logits=lg, C=256)
+    check_full(G, r, T, 8, True)
+    assert np.array_equal(out.view(np.uint32), r["out"].view(np.uint32))
+    G.close()
+
+
+def test_router_logits_bit_exact(gpu):
+    T = 70
+    say(f"[router logits] T={T}")
+    L = layer_for("mixed", True)
+    G = make_gpu_layer(L, 256)
+    x = synth.make_x(3, T)
+    run_layer(G, x, gpu)
+    part = G.read("logits_part", (8, T, 256), np.float32)
+    lg = part[0].copy()
+    for c in range(1, 8):
+        lg = (lg + part[c]).astype(np.float32)
+    ref = oracle.router_logits(x, L["Wr"])
+    assert np.array_equal(lg.view(np.uint32), ref.view(np.uint32))
+    G.close()
+
+
+def test_external_dispatch(gpu):
+    """llmoe_dispatch + llmoe_experts with externally given routing (uniform random distinct experts)."""
+    import torch
+    T, K = 64, 8
+    say(f"[dispatch] T={T}")
+    L = layer_for("mixed", True)
+    G = make_gpu_layer(L, 256)
+    rng = np.random.default_rng(9)
+    topk = np.stack([rng.choice(256, K, replace=False) for _ in range(T)]).astype(np.int32)
+    topw = rng.uniform(0.05, 0.6, (T, K)).astype(np.float32)
+    x = synth.make_x(4, T)
+    xq, xs, xsum = oracle.quant_a8(x)
+    G.dispatch(to_dev(topk, gpu), to_dev(topw, gpu))
+    out = G.experts(to_dev(xq, gpu), to_dev(xs, gpu), to_dev(xsum, gpu))
+    torch.cuda.synchronize()
+    r = oracle.Layer(L).experts(xq, xs, xsum, topk, topw)
+    r.update(topk=topk, topw=topw)
+    check_full(G, r, T, K, True)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), r["out"].view(np.uint32))
+    G.close()
