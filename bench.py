@@ -1,0 +1,251 @@
+#!/usr/bin/env python3
+"""Benchmark of the LLaDA2 routed-expert MoE layer on one MI355X through libllmoe.so.
+
+Headline workload (value): BASELINE config 1 -- one MoE layer, 32 tokens (one denoising block), hidden 2048,
+256 routed experts at the shipped 2/3/4-bit mix (61/34/6 %), top-8 of sigmoid(x Wr) + bias, plus the W8A8
+shared expert; a step is one full layer pass (A8 of x -> router -> routing + dispatch -> gate_up -> FWHT-512 + A8
+-> down -> combine) with x already resident in HBM. Also measured (fields "configs"): config 0 (32 tokens, all
+4-bit, block pool 48, no shared expert) and config 3 (2048 tokens through a stack of 20 independently seeded
+layers with Zipf(1.1) expert load).
+
+Roofline: the dominant kernel is the gate_up expert GEMM (two thirds of the weight bytes); its algorithmic bytes
+per launch are the packed gate_up bytes of every expert the step touches (each streamed exactly once) plus the
+shared expert's, and its duration is measured with HIP events on the launch stream (llmoe_layer_stage_ms).
+
+CPU baseline: the CPU oracle (oracle/, the C restatement of the reference's path, OpenMP over experts) timed on
+the host cores on the same config-1 layer and input, repeated for a bounded ~10 s.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path[:0] = [str(ROOT / "llada2-orin-cuda_amd"), str(ROOT / "oracle")]
+
+import numpy as np  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+PEAK_INT8_TOPS = 5000.0        # MI355X dense int8 MFMA (TOP/s)
+H, I, K, E = 2048, 512, 8, 256
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_gpu_layer(llmoe, L, pool, max_tokens):
+    return llmoe.Layer(L["blob"], L["gu_off"], L["d_off"], L["bits"], L["bias"], L["Wr"], n_experts=E, top_k=K,
+                       pool=pool, has_shared=L["shared"], max_tokens=max_tokens)
+
+
+def gate_up_bytes(L, topk):
+    from llmoe import synth
+    used = np.unique(topk.reshape(-1))
+    b = sum(synth.matrix_bytes(2 * I, H, int(L["bits"][e])) for e in used)
+    if L["shared"]:
+        b += synth.matrix_bytes(2 * I, H, 8)
+    return int(b)
+
+
+def down_bytes(L, topk):
+    from llmoe import synth
+    used = np.unique(topk.reshape(-1))
+    b = sum(synth.matrix_bytes(H, I, int(L["bits"][e])) for e in used)
+    if L["shared"]:
+        b += synth.matrix_bytes(H, I, 8)
+    return int(b)
+
+
+def time_steps(fn, steps, warmup):
+    """fn(i) runs step i; W untimed warmup steps, then exactly `steps` timed steps between synchronisations."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+def stage_profile(G, fn, reps=20):
+    import torch
+    G.set_profiling(True)
+    acc = {}
+    for i in range(reps):
+        fn(i)
+        for k, v in G.stage_ms().items():
+            acc.setdefault(k, []).append(v)
+    G.set_profiling(False)
+    torch.cuda.synchronize()
+    return {k: float(np.median(v)) for k, v in acc.items()}
+
+
+def one_layer_config(llmoe, synth, torch, name, seed, T, mix, shared, pool, steps, warmup, nlayers=4):
+    """A step is one layer pass; consecutive steps cycle through `nlayers` independently seeded layers so the
+    weights (> 256 MB in total) stream from HBM, not from the last-level cache."""
+    dev = torch.device("cuda:0")
+    Ls = [synth.make_layer(seed + 1000 * i, mix=mix, shared=shared) for i in range(nlayers)]
+    Gs = [make_gpu_layer(llmoe, L, pool, T) for L in Ls]
+    x = torch.from_numpy(synth.make_x(seed + 1, T)).to(dev)
+    out = torch.empty((T, H), dtype=torch.float32, device=dev)
+    fn = lambda i: Gs[i % nlayers].forward(x, out=out)  # noqa: E731
+    dt = time_steps(fn, steps, warmup)
+    prof = stage_profile(Gs[0], lambda i: Gs[0].forward(x, out=out))
+    for G in Gs:
+        G.forward(x, out=out)
+    # steady-state kernel durations: back-to-back launches cycling through the layers, between two HIP events on
+    # the launch stream
+    prof["gate_up"] = llmoe.time_stage_layers(Gs, "gate_up", 20)
+    prof["down"] = llmoe.time_stage_layers(Gs, "down", 20)
+    topks = [G.read("topk", (T, K), np.int32) for G in Gs]
+    gub = float(np.mean([gate_up_bytes(L, t) for L, t in zip(Ls, topks)]))
+    dnb = float(np.mean([down_bytes(L, t) for L, t in zip(Ls, topks)]))
+    slots = T * K + (T if shared else 0)
+    t_w = (prof["gate_up"] + prof["down"]) * 1e-3
+    res = {
+        "workload": name, "tokens": T, "layers_cycled": nlayers, "ms_per_step": dt / steps * 1e3,
+        "tokens_per_s": T * steps / dt, "experts_touched": float(np.mean([np.unique(t).size for t in topks])),
+        "weight_bytes": gub + dnb, "weight_stream_GBps": (gub + dnb) / t_w / 1e9,
+        "weight_stream_frac_peak": (gub + dnb) / t_w / 1e9 / PEAK_HBM_GBS,
+        "int8_TOPS": 2 * slots * 3 * I * H / t_w / 1e12,
+        "stage_ms": prof, "gate_up_bytes": gub, "down_bytes": dnb,
+    }
+    return res, (Ls[0], Gs, x, out, fn)
+
+
+def stack_config(llmoe, synth, torch, steps, warmup, nlayers=20, T=2048):
+    """Config 3: 2048 tokens through 20 independently seeded mixed-bit layers (+ shared), Zipf(1.1) load."""
+    dev = torch.device("cuda:0")
+    layers, logits = [], []
+    wbytes = 0
+    t0 = time.perf_counter()
+    for li in range(nlayers):
+        L = synth.make_layer(1000 + li, mix="mixed", shared=True, zero_bias=True)
+        layers.append((L, make_gpu_layer(llmoe, L, 256, T)))
+        logits.append(torch.from_numpy(synth.logits_zipf(2000 + li, T)).to(dev))
+        del L["blob"]
+    log(f"[bench] config 3: {nlayers} layers built in {time.perf_counter() - t0:.1f} s")
+    x = torch.from_numpy(synth.make_x(7, T)).to(dev)
+    out = torch.empty((T, H), dtype=torch.float32, device=dev)
+
+    def fn(i):
+        for (L, G), lg in zip(layers, logits):
+            G.forward(x, lg, out=out)
+
+    dt = time_steps(fn, steps, warmup)
+    # per-layer stage profile and weight bytes
+    for (L, G), lg in zip(layers, logits):
+        G.forward(x, lg, out=out)
+        topk = G.read("topk", (T, K), np.int32)
+        wbytes += gate_up_bytes(L, topk) + down_bytes(L, topk)
+    Gs = [G for _, G in layers]
+    gu = llmoe.time_stage_layers(Gs, "gate_up", 3)
+    dn = llmoe.time_stage_layers(Gs, "down", 3)
+    gu_ms, dn_ms = [gu] * nlayers, [dn] * nlayers
+    t_w = (sum(gu_ms) + sum(dn_ms)) * 1e-3
+    slots = T * (K + 1) * nlayers
+    res = {
+        "workload": "config 3: 2048 tokens x 20 layers, mixed 2/3/4-bit + W8A8 shared, Zipf(1.1) load",
+        "tokens": T, "layers": nlayers, "ms_per_step": dt / steps * 1e3,
+        "tokens_per_s_per_layer": T * nlayers * steps / dt, "stack_tokens_per_s": T * steps / dt,
+        "weight_bytes": wbytes, "weight_stream_GBps": wbytes / t_w / 1e9,
+        "weight_stream_frac_peak": wbytes / t_w / 1e9 / PEAK_HBM_GBS,
+        "int8_TOPS": 2 * slots * 3 * I * H / t_w / 1e12,
+        "int8_mfma_frac_peak": 2 * slots * 3 * I * H / t_w / 1e12 / PEAK_INT8_TOPS,
+        "gate_up_ms_per_layer": float(np.mean(gu_ms)), "down_ms_per_layer": float(np.mean(dn_ms)),
+    }
+    for _, G in layers:
+        G.close()
+    return res
+
+
+def cpu_baseline(L, x_np, pool, seconds):
+    import oracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    O = oracle.Layer(L)
+    T = x_np.shape[0]
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.forward(x_np, C=pool, nthreads=threads)
+        n += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": T * n / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n} full passes of the config-1 layer ({T} tokens) through the C oracle "
+                      f"(A8, fixed-order router, routing, integer W*A8 experts, FWHT-512, combine), {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-stack", action="store_true", help="skip config 3 (20-layer, 2048-token stack)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only-headline", action="store_true", help="config 1 only (profiling runs)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (expert sharding is described in "
+              "DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import llmoe
+    from llmoe import synth
+    llmoe.load_library()
+    torch.cuda.set_device(0)
+
+    log("[bench] config 1 (headline)")
+    c1, (L1, G1s, x1, _, _) = one_layer_config(llmoe, synth, torch, "config 1: 32 tokens, mixed 2/3/4-bit + W8A8 "
+                                              "shared, uniform-random routing (no pool)", 1, 32, "mixed", True, 256,
+                                              args.steps, args.warmup)
+    configs = [c1]
+    if not args.only_headline:
+        log("[bench] config 0")
+        c0, (_, G0s, _, _, _) = one_layer_config(llmoe, synth, torch, "config 0: 32 tokens, 4-bit, pool 48, "
+                                                 "no shared", 11, 32, 4, False, 48, args.steps, args.warmup)
+        for G in G0s:
+            G.close()
+        configs.insert(0, c0)
+    if not args.no_stack and not args.only_headline:
+        log("[bench] config 3")
+        configs.append(stack_config(llmoe, synth, torch, max(1, args.steps // 20), max(1, args.warmup // 10)))
+
+    p = c1["stage_ms"]
+    gu_s = p["gate_up"] * 1e-3
+    achieved = c1["gate_up_bytes"] / gu_s / 1e9
+    roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                "kernel": "stream_gemm<gate_up> (config 1)", "bytes_per_launch": c1["gate_up_bytes"],
+                "avg_launch_ms": p["gate_up"]}
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        cpu = cpu_baseline(L1, x1.cpu().numpy(), 256, args.cpu_seconds)
+    for G in G1s:
+        G.close()
+    line = {
+        "metric": "MoE-layer tokens/sec at 32 & 2048 tokens; weight-stream HBM GB/s as % peak",
+        "value": c1["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": c1["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic (seeded random packed weights and activations of the config shapes)",
+        "config": {"workload": c1["workload"], "tokens": 32, "hidden": H, "inter": I, "experts": E, "top_k": K,
+                   "parallelism": "single GPU"},
+        "weight_stream_GBps": c1["weight_stream_GBps"], "weight_stream_frac_peak": c1["weight_stream_frac_peak"],
+        "roofline": roofline, "cpu_baseline": cpu, "configs": configs,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

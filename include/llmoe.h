@@ -122,6 +122,34 @@ int llmoe_layer_weight_bytes(const llmoe_layer* layer, size_t* bytes);
 int llmoe_group_products(llmoe_layer* layer, int expert, int which, const int8_t* xq, const int32_t* xsum, int n,
                          int32_t* P, llmoe_stream stream);
 
+/* Per-stage timing (the analogue of Engine::mark / prof_collect, engine/engine.cu:385-407, enabled there by
+ * PROF=1): while enabled, every stage of the layer's calls is bracketed by HIP events on the call's stream.
+ * Not for use under graph capture. llmoe_layer_stage_ms waits for the last recorded stage and returns, per
+ * stage, the milliseconds of its latest run (-1 if it has not run since profiling was enabled).
+ * Stages: LLMOE_STAGE_* below. */
+#define LLMOE_STAGE_QUANT 0
+#define LLMOE_STAGE_ROUTER 1
+#define LLMOE_STAGE_ROUTE 2
+#define LLMOE_STAGE_DISPATCH 3
+#define LLMOE_STAGE_GATE_UP 4
+#define LLMOE_STAGE_FWHT 5
+#define LLMOE_STAGE_DOWN 6
+#define LLMOE_STAGE_COMBINE 7
+#define LLMOE_N_STAGES 8
+int llmoe_layer_set_profiling(llmoe_layer* layer, int enabled);
+int llmoe_layer_stage_ms(llmoe_layer* layer, float* ms);
+
+/* Re-launch one expert stage of the latest llmoe_experts call (LLMOE_STAGE_GATE_UP, _FWHT, _DOWN or _COMBINE)
+ * `reps` times back to back between two HIP events on `stream`, and return the average milliseconds per
+ * launch (the kernel's steady-state duration; the stages are idempotent). Waits for completion. */
+int llmoe_layer_time_stage(llmoe_layer* layer, int stage, int reps, llmoe_stream stream, float* avg_ms);
+
+/* As llmoe_layer_time_stage over n layers launched in turn (layer 0, 1, .., n-1, repeated `reps` times): with
+ * more weight bytes than the GPU's last-level cache (256 MB on MI355X) every launch streams from HBM.
+ * avg_ms = milliseconds per launch. */
+int llmoe_layers_time_stage(llmoe_layer* const* layers, int n, int stage, int reps, llmoe_stream stream,
+                            float* avg_ms);
+
 /* Message of the calling thread's last error ("" if none). */
 const char* llmoe_last_error(void);
 

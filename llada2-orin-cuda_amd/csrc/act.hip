@@ -115,17 +115,27 @@ __global__ void __launch_bounds__(256) fwht_a8_kernel(const uint16_t* __restrict
 }
 
 // out[t, :] = sum_{k < kk} Y[tok_slots[t, k], :], k ascending (engine/moe_i8.cu:505-515). grid T, 256 threads.
+constexpr int MAX_KK = 9;   // top-8 + the shared expert
 __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ Y, const int* __restrict__ tok_slots,
                                                       int H, int kk, int K1, float* __restrict__ out) {
     const int t = blockIdx.x;
+    int sl[MAX_KK];
+#pragma unroll
+    for (int k = 0; k < MAX_KK; ++k) sl[k] = k < kk ? tok_slots[t * K1 + k] : 0;
     for (int h = threadIdx.x * 4; h < H; h += blockDim.x * 4) {
+        float4 v[MAX_KK];
+#pragma unroll
+        for (int k = 0; k < MAX_KK; ++k)   // every load in flight before the ordered sum
+            if (k < kk) v[k] = *reinterpret_cast<const float4*>(Y + size_t(sl[k]) * H + h);
         float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (int k = 0; k < kk; ++k) {
-            const float4 v = *reinterpret_cast<const float4*>(Y + size_t(tok_slots[t * K1 + k]) * H + h);
-            acc.x = acc.x + v.x;
-            acc.y = acc.y + v.y;
-            acc.z = acc.z + v.z;
-            acc.w = acc.w + v.w;
+#pragma unroll
+        for (int k = 0; k < MAX_KK; ++k) {
+            if (k < kk) {
+                acc.x = acc.x + v[k].x;
+                acc.y = acc.y + v[k].y;
+                acc.z = acc.z + v[k].z;
+                acc.w = acc.w + v[k].w;
+            }
         }
         *reinterpret_cast<float4*>(out + size_t(t) * H + h) = acc;
     }

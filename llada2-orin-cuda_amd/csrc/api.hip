@@ -73,6 +73,15 @@ struct llmoe_layer {
     size_t items_cap = 0;
     // routing state
     int routed_T = -1, ntok = 16, max_items = 0;
+    // stage timing
+    bool profiling = false;
+    hipEvent_t ev[2 * LLMOE_N_STAGES] = {};
+    bool ran[LLMOE_N_STAGES] = {};
+    // the latest llmoe_experts launch (for llmoe_layer_time_stage)
+    GemmArgs last_gu{}, last_dn{};
+    float* last_out = nullptr;
+    int last_S = 0, last_T = 0, last_nt = 1;
+    bool have_last = false;
     std::vector<void*> allocs;
 
     template <class T>
@@ -86,7 +95,14 @@ struct llmoe_layer {
         return e;
     }
     ~llmoe_layer() {
+        for (hipEvent_t e : ev)
+            if (e) (void)hipEventDestroy(e);
         for (void* p : allocs) (void)hipFree(p);
+    }
+    void mark(int stage, bool end, hipStream_t st) {
+        if (!profiling) return;
+        (void)hipEventRecord(ev[2 * stage + (end ? 1 : 0)], st);
+        if (end) ran[stage] = true;
     }
 };
 
@@ -116,14 +132,21 @@ int check_T(const llmoe_layer* L, int T) {
     return LLMOE_OK;
 }
 
+// expert GEMM of one stage (items of 16 * nt slots)
+hipError_t launch_gemm(int mode, int nt, const GemmArgs& g, int max_items, hipStream_t st) {
+    return launch_expert_gemm(mode, nt, g, max_items, st);
+}
+
 int plan_and_place(llmoe_layer* L, const int32_t* topk, const float* topw, int T, hipStream_t st) {
     const auto& d = L->d;
     choose_items(L, T);
     if (size_t(L->max_items) > L->items_cap) return fail(LLMOE_EINVAL, "item capacity exceeded");
+    L->mark(LLMOE_STAGE_DISPATCH, false, st);
     HIPCHECK(launch_plan(L->mask, T, d.n_experts, d.top_k, d.block, d.has_shared, L->ntok, L->count, L->start, L->bpre,
                          L->items, L->n_items, st));
     HIPCHECK(launch_place(topk, topw, L->mask, L->bpre, T, d.n_experts, d.top_k, d.block, d.has_shared,
                           L->slot_token, L->slot_weight, L->tok_slots, st));
+    L->mark(LLMOE_STAGE_DISPATCH, true, st);
     L->routed_T = T;
     return LLMOE_OK;
 }
@@ -281,12 +304,27 @@ int llmoe_route(llmoe_layer* L, const float* x, const float* logits, int T, llmo
     int nchunks = 1;
     if (x) {
         if (!L->router_w) return fail(LLMOE_EINVAL, "layer created without a router matrix");
+        L->mark(LLMOE_STAGE_ROUTER, false, st);
         HIPCHECK(launch_router_logits(x, L->router_w, T, d.hidden, d.n_experts, L->part, st));
+        L->mark(LLMOE_STAGE_ROUTER, true, st);
         part = L->part;
         nchunks = ROUTER_KC;
     }
+    L->mark(LLMOE_STAGE_ROUTE, false, st);
+    if (T <= d.block) {   // one routing block (a decode step): route, plan and place in one workgroup
+        choose_items(L, T);
+        if (size_t(L->max_items) > L->items_cap) return fail(LLMOE_EINVAL, "item capacity exceeded");
+        HIPCHECK(launch_route_dispatch(part, nchunks, L->bias, T, d.n_experts, d.top_k, d.pool, d.block,
+                                       d.routed_scale, L->topk, L->topw, L->mask, d.has_shared, L->ntok, L->bits_d,
+                                       L->count, L->start, L->items, L->n_items, L->slot_token, L->slot_weight,
+                                       L->tok_slots, st));
+        L->mark(LLMOE_STAGE_ROUTE, true, st);
+        L->routed_T = T;
+        return LLMOE_OK;
+    }
     HIPCHECK(launch_route(part, nchunks, L->bias, T, d.n_experts, d.top_k, d.pool, d.block, d.routed_scale, L->topk,
                           L->topw, L->mask, st));
+    L->mark(LLMOE_STAGE_ROUTE, true, st);
     return plan_and_place(L, L->topk, L->topw, T, st);
 }
 
@@ -324,15 +362,26 @@ int llmoe_experts(llmoe_layer* L, const int8_t* xq, const float* xs, const int32
     g.slot_token = L->slot_token;
     g.xq = xq; g.xs = xs; g.xsum = xsum;
     g.K = H; g.R = 2 * I; g.Z = L->Z;
-    HIPCHECK(launch_expert_gemm(GEMM_GATE_UP, nt, g, L->max_items, st));
+    L->last_gu = g;
+    L->mark(LLMOE_STAGE_GATE_UP, false, st);
+    HIPCHECK(launch_gemm(GEMM_GATE_UP, nt, g, L->max_items, st));
+    L->mark(LLMOE_STAGE_GATE_UP, true, st);
+    L->mark(LLMOE_STAGE_FWHT, false, st);
     HIPCHECK(launch_fwht_a8(L->Z, S, L->zq, L->zs, L->zsum, st));
+    L->mark(LLMOE_STAGE_FWHT, true, st);
     // down: B rows are slot rows of Z'
     g.off = L->d_off_d;
     g.slot_token = nullptr;
     g.xq = L->zq; g.xs = L->zs; g.xsum = L->zsum;
     g.K = I; g.R = H; g.Z = nullptr; g.Y = L->Y;
-    HIPCHECK(launch_expert_gemm(GEMM_DOWN, nt, g, L->max_items, st));
+    L->last_dn = g;
+    L->last_S = S; L->last_T = T; L->last_nt = nt; L->last_out = out; L->have_last = true;
+    L->mark(LLMOE_STAGE_DOWN, false, st);
+    HIPCHECK(launch_gemm(GEMM_DOWN, nt, g, L->max_items, st));
+    L->mark(LLMOE_STAGE_DOWN, true, st);
+    L->mark(LLMOE_STAGE_COMBINE, false, st);
     HIPCHECK(launch_combine(L->Y, L->tok_slots, T, H, K + (d.has_shared ? 1 : 0), K + 1, out, st));
+    L->mark(LLMOE_STAGE_COMBINE, true, st);
     return LLMOE_OK;
 }
 
@@ -340,9 +389,81 @@ int llmoe_layer_forward(llmoe_layer* L, const float* x, const float* logits, int
     if (int rc = check_layer(L)) return rc;
     if (int rc = check_T(L, T)) return rc;
     if (!x || !out) return fail(LLMOE_EINVAL, "null argument");
+    L->mark(LLMOE_STAGE_QUANT, false, static_cast<hipStream_t>(stream));
     if (int rc = llmoe_quantize_a8(x, T, L->d.hidden, L->xq, L->xs, L->xsum, stream)) return rc;
+    L->mark(LLMOE_STAGE_QUANT, true, static_cast<hipStream_t>(stream));
     if (int rc = llmoe_route(L, logits ? nullptr : x, logits, T, stream)) return rc;
     return llmoe_experts(L, L->xq, L->xs, L->xsum, T, out, stream);
+}
+
+int llmoe_layer_set_profiling(llmoe_layer* L, int enabled) {
+    if (int rc = check_layer(L)) return rc;
+    if (enabled) {
+        for (hipEvent_t& e : L->ev)
+            if (!e) HIPCHECK(hipEventCreate(&e));
+        for (bool& r : L->ran) r = false;
+    }
+    L->profiling = enabled != 0;
+    return LLMOE_OK;
+}
+
+int llmoe_layer_stage_ms(llmoe_layer* L, float* ms) {
+    if (int rc = check_layer(L)) return rc;
+    if (!ms) return fail(LLMOE_EINVAL, "null argument");
+    for (int i = 0; i < LLMOE_N_STAGES; ++i) {
+        ms[i] = -1.0f;
+        if (!L->ran[i]) continue;
+        HIPCHECK(hipEventSynchronize(L->ev[2 * i + 1]));
+        HIPCHECK(hipEventElapsedTime(&ms[i], L->ev[2 * i], L->ev[2 * i + 1]));
+    }
+    return LLMOE_OK;
+}
+
+namespace {
+hipError_t relaunch_stage(llmoe_layer* L, int stage, hipStream_t st) {
+    const auto& d = L->d;
+    switch (stage) {
+        case LLMOE_STAGE_GATE_UP: return launch_gemm(GEMM_GATE_UP, L->last_nt, L->last_gu, L->max_items, st);
+        case LLMOE_STAGE_DOWN: return launch_gemm(GEMM_DOWN, L->last_nt, L->last_dn, L->max_items, st);
+        case LLMOE_STAGE_FWHT: return launch_fwht_a8(L->Z, L->last_S, L->zq, L->zs, L->zsum, st);
+        case LLMOE_STAGE_COMBINE:
+            return launch_combine(L->Y, L->tok_slots, L->last_T, d.hidden, d.top_k + (d.has_shared ? 1 : 0),
+                                  d.top_k + 1, L->last_out, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+}  // namespace
+
+int llmoe_layers_time_stage(llmoe_layer* const* layers, int n, int stage, int reps, llmoe_stream stream,
+                            float* avg_ms) {
+    if (!layers || n < 1 || !avg_ms || reps < 1) return fail(LLMOE_EINVAL, "bad argument");
+    if (stage != LLMOE_STAGE_GATE_UP && stage != LLMOE_STAGE_DOWN && stage != LLMOE_STAGE_FWHT &&
+        stage != LLMOE_STAGE_COMBINE)
+        return fail(LLMOE_EINVAL, "stage %d cannot be re-launched", stage);
+    for (int i = 0; i < n; ++i) {
+        if (int rc = check_layer(layers[i])) return rc;
+        if (!layers[i]->have_last) return fail(LLMOE_ESTATE, "layer %d: no llmoe_experts call to repeat", i);
+    }
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    hipEvent_t a, b;
+    HIPCHECK(hipEventCreate(&a));
+    HIPCHECK(hipEventCreate(&b));
+    for (int i = 0; i < n; ++i) HIPCHECK(relaunch_stage(layers[i], stage, st));   // warm
+    HIPCHECK(hipEventRecord(a, st));
+    for (int r = 0; r < reps; ++r)
+        for (int i = 0; i < n; ++i) HIPCHECK(relaunch_stage(layers[i], stage, st));
+    HIPCHECK(hipEventRecord(b, st));
+    HIPCHECK(hipEventSynchronize(b));
+    float ms = 0.0f;
+    HIPCHECK(hipEventElapsedTime(&ms, a, b));
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    *avg_ms = ms / float(reps * n);
+    return LLMOE_OK;
+}
+
+int llmoe_layer_time_stage(llmoe_layer* L, int stage, int reps, llmoe_stream stream, float* avg_ms) {
+    return llmoe_layers_time_stage(&L, 1, stage, reps, stream, avg_ms);
 }
 
 int llmoe_layer_buffers(const llmoe_layer* L, llmoe_buffers* o) {

@@ -14,6 +14,8 @@
 //                     (engine/moe_i8.cu:219-221)
 //   down    (MODE 1): rows H = 2048, K = I = 512, SPW 4;  out Y[slot, h] = w_slot acc (engine/moe_i8.cu:222-231)
 //   products (MODE 2, 3): raw P_g per (token, row, group) in either geometry, for the bit-exactness test.
+#include <type_traits>
+
 #include "llmoe_internal.h"
 
 namespace llmoe {
@@ -25,22 +27,23 @@ typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 
 constexpr int WAVES = 4;
 
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
 template <int BITS>
-struct Step {               // one strip-superblock of one lane: codes + meta
+struct Step {               // the code bytes of one strip-superblock held by one lane (meta comes from LDS)
     u4 c[BITS];
-    u4 s0, s1;              // fp16 scales: s0 = tiles 0,1; s1 = tiles 2,3 (4 rows each)
-    u4 z;                   // u8 zeros: word tau = rows 0..3 of tile tau
 };
 
 template <int BITS>
 __device__ __forceinline__ void load_step(const uint8_t* sbp, int lane, Step<BITS>& r) {
-    const int q = lane >> 4;
 #pragma unroll
     for (int i = 0; i < BITS; ++i) r.c[i] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(sbp + i * 1024) + lane);
-    const uint8_t* meta = sbp + BITS * 1024;
-    r.s0 = *reinterpret_cast<const u4*>(meta + 32 * q);
-    r.s1 = *reinterpret_cast<const u4*>(meta + 32 * q + 16);
-    r.z = *reinterpret_cast<const u4*>(meta + 128 + 16 * q);
 }
 
 __device__ __forceinline__ uint32_t wsel(const u4& v, int i) { return v[i]; }
@@ -80,6 +83,15 @@ __device__ __forceinline__ void unpack_tile(const Step<BITS>& r, int tau, uint32
     }
 }
 
+// f32(fp16 half `hi` of `packed`) * x with one rounding (v_fma_mix_f32 with addend -0: exactly the fp32 product,
+// including the sign of zero), i.e. the same value as converting the scale and multiplying
+__device__ __forceinline__ float mul_f16_f32(uint32_t packed, int hi, float x) {
+    float r;
+    if (hi) asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(x), "v"(-0.0f));
+    else asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(x), "v"(-0.0f));
+    return r;
+}
+
 // packlib strip row of device gate_up strip row d (inverse of the interleave written by relayout.hip)
 __device__ __forceinline__ int gu_packlib_row(int d) {
     const int q = d >> 2, v = d & 3;
@@ -91,19 +103,28 @@ struct Geo {
     static constexpr bool DOWN_SHAPE = MODE == GEMM_DOWN || MODE == GEMM_PRODUCTS_DOWN;
     static constexpr bool PRODUCTS = MODE == GEMM_PRODUCTS_GATE_UP || MODE == GEMM_PRODUCTS_DOWN;
     static constexpr int NSB = DOWN_SHAPE ? 1 : 4;       // K = 512 or 2048
-    static constexpr int SPW = DOWN_SHAPE ? 4 : 1;
+    static constexpr int SPW = DOWN_SHAPE ? 8 : 4;       // strips per wave, streamed as one ring
 };
 
+// ring depth (superblock steps in flight per wave), a divisor of 4. Registers hold only code bytes (the
+// group scales and zeros are staged in LDS), so a wave keeps 4 steps -- 8 to 16 KiB -- in flight.
 template <int BITS>
 struct Ring {
-    static constexpr int D = BITS <= 3 ? 4 : BITS == 4 ? 3 : 2;
+    static constexpr int D = BITS == 8 ? 2 : 4;
 };
 
-__host__ __device__ constexpr int lds_bytes(int ntok, int K) { return ntok * (K + 16) + ntok * (K / GROUP) * 8; }
+// LDS: B rows [ntok][K + 16], B scales and sums [K/128][ntok] x 2, then the meta of the workgroup's
+// superblocks [strip][superblock][192 B]
+__host__ __device__ constexpr int b_bytes(int ntok, int K) { return ntok * (K + 16) + ntok * (K / GROUP) * 8; }
+template <int MODE>
+__host__ __device__ constexpr int meta_bytes() { return WAVES * Geo<MODE>::SPW * Geo<MODE>::NSB * META_SB; }
+template <int MODE, int NT>
+__host__ __device__ constexpr int lds_bytes() { return b_bytes(16 * NT, Geo<MODE>::NSB * SB_K) + meta_bytes<MODE>(); }
 
 template <int BITS, int MODE, int NT>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uint8_t* lds, int row_block) {
     constexpr int NSB = Geo<MODE>::NSB, SPW = Geo<MODE>::SPW, NSTEP = NSB * SPW, D = Ring<BITS>::D;
+    static_assert(NSTEP % 4 == 0 && 4 % D == 0, "ring geometry");
     constexpr int K = NSB * SB_K, G = K / GROUP, NTOK = 16 * NT, LDQ = K + 16;
     constexpr size_t SBB = sb_bytes(BITS);
     constexpr int ZOFF = BITS == 8 ? 128 : 0;
@@ -111,41 +132,97 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
     const int strip0 = (row_block * WAVES + wave) * SPW;
     const uint8_t* mat = a.base + a.off[it.expert] + size_t(strip0) * NSB * SBB;
 
-    // weight prefetch first: its latency overlaps the B staging below
+    // weight prefetch first: its latency overlaps the meta and B staging below
     Step<BITS> ring[D];
 #pragma unroll
     for (int u = 0; u < D; ++u)
         if (u < NSTEP) load_step<BITS>(mat + size_t(u) * SBB, lane, ring[u]);
+
+    // meta (scales, zeros) of every superblock of the workgroup's strips -> LDS
+    uint8_t* meta_lds = lds + b_bytes(NTOK, K);
+    {
+        constexpr int NMETA = WAVES * SPW * NSB * (META_SB / 16);   // 16-byte chunks
+        constexpr int PM = (NMETA + WAVES * 64 - 1) / (WAVES * 64);
+        const uint8_t* wg_mat = a.base + a.off[it.expert] + size_t(row_block * WAVES * SPW) * NSB * SBB;
+        u4 mv[PM];
+#pragma unroll
+        for (int i = 0; i < PM; ++i) {
+            const int idx = threadIdx.x + i * WAVES * 64;
+            if (idx < NMETA) mv[i] = *reinterpret_cast<const u4*>(wg_mat + size_t(idx / 12) * SBB + BITS * 1024 + 16 * (idx % 12));
+        }
+#pragma unroll
+        for (int i = 0; i < PM; ++i) {
+            const int idx = threadIdx.x + i * WAVES * 64;
+            if (idx < NMETA) *reinterpret_cast<u4*>(meta_lds + 16 * idx) = mv[i];
+        }
+    }
 
     // stage the item's B rows in LDS: q8 rows [NTOK][LDQ], scales [G][NTOK], sums [G][NTOK]
     int8_t* bq = reinterpret_cast<int8_t*>(lds);
     float* bs = reinterpret_cast<float*>(lds + NTOK * LDQ);
     int* bsum = reinterpret_cast<int*>(bs + G * NTOK);
     const int ntok = it.ntok;
-    for (int v = threadIdx.x; v < ntok * (K / 16); v += WAVES * 64) {
-        const int n = v / (K / 16), c16 = v % (K / 16);
-        const int slot = it.slot0 + n;
-        const size_t row = a.slot_token ? size_t(a.slot_token[slot]) : size_t(slot);
-        *reinterpret_cast<uint4*>(bq + n * LDQ + 16 * c16) = *reinterpret_cast<const uint4*>(a.xq + row * K + 16 * c16);
-    }
-    for (int v = threadIdx.x; v < ntok * G; v += WAVES * 64) {
-        const int n = v / G, g = v % G;
-        const int slot = it.slot0 + n;
-        const size_t row = a.slot_token ? size_t(a.slot_token[slot]) : size_t(slot);
-        bs[g * NTOK + n] = a.xs ? a.xs[row * G + g] : 0.0f;
-        bsum[g * NTOK + n] = a.xsum[row * G + g];
+    {
+        // B rows: NTOK * K / 16 chunks of 16 bytes over 256 threads; all loads issued before the LDS stores
+        constexpr int CH = K / 16, PER = (NTOK * CH + WAVES * 64 - 1) / (WAVES * 64);
+        u4 v[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = threadIdx.x + i * WAVES * 64, n = idx / CH, c16 = idx % CH;
+            if (n < ntok) {
+                const int slot = it.slot0 + n;
+                const size_t row = a.slot_token ? size_t(a.slot_token[slot]) : size_t(slot);
+                v[i] = *reinterpret_cast<const u4*>(a.xq + row * K + 16 * c16);
+            }
+        }
+        constexpr int PG = (NTOK * G + WAVES * 64 - 1) / (WAVES * 64);
+        float sv[PG];
+        int qv[PG];
+#pragma unroll
+        for (int i = 0; i < PG; ++i) {
+            const int idx = threadIdx.x + i * WAVES * 64, n = idx / G, g = idx % G;
+            if (n < ntok) {
+                const int slot = it.slot0 + n;
+                const size_t row = a.slot_token ? size_t(a.slot_token[slot]) : size_t(slot);
+                sv[i] = a.xs ? a.xs[row * G + g] : 0.0f;
+                qv[i] = a.xsum[row * G + g];
+            }
+        }
+        // rows n >= ntok are zero: the MFMA columns of absent tokens then compute zeros, branch-free
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = threadIdx.x + i * WAVES * 64, n = idx / CH, c16 = idx % CH;
+            if (n < NTOK) *reinterpret_cast<u4*>(bq + n * LDQ + 16 * c16) = n < ntok ? v[i] : u4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < PG; ++i) {
+            const int idx = threadIdx.x + i * WAVES * 64, n = idx / G, g = idx % G;
+            if (n < NTOK) {
+                bs[g * NTOK + n] = n < ntok ? sv[i] : 0.0f;
+                bsum[g * NTOK + n] = n < ntok ? -qv[i] : 0;          // negated: C = zero * (-sum)
+            }
+        }
     }
     __syncthreads();
 
-    float acc[NT][4];
+    float acc[NT][4], tot[NT][4];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[nt][0] = acc[nt][1] = acc[nt][2] = acc[nt][3] = 0.0f;
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[nt][v] = tot[nt][v] = 0.0f;
 
-#pragma unroll
-    for (int u = 0; u < NSTEP; ++u) {
-        const Step<BITS> cur = ring[u % D];
-        if (u + D < NSTEP) load_step<BITS>(mat + size_t(u + D) * SBB, lane, ring[u % D]);
-        const int sb = u % NSB, strip = strip0 + u / NSB;
+    // the wave's SPW strips are NSTEP consecutive superblocks in memory, streamed as one ring (slot of step u =
+    // u % D). The steps are unrolled at compile time: across a loop back-edge the compiler would wait for every
+    // outstanding load, and the prefetch would not overlap.
+    static_for<0, NSTEP>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        Step<BITS>& cur = ring[u % D];
+        constexpr int sb = u % NSB;
+        const int strip = strip0 + u / NSB;
+        const uint8_t* mp = meta_lds + (size_t(strip - row_block * WAVES * SPW) * NSB + sb) * META_SB;
+        const u4 ms0 = *reinterpret_cast<const u4*>(mp + 32 * q);
+        const u4 ms1 = *reinterpret_cast<const u4*>(mp + 32 * q + 16);
+        const u4 zw4 = *reinterpret_cast<const u4*>(mp + 128 + 16 * q);
 #pragma unroll
         for (int tau = 0; tau < 4; ++tau) {
             const int g = sb * 4 + tau;
@@ -153,31 +230,29 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
             unpack_tile<BITS>(cur, tau, Dw);
             const v4i A0 = {int(Dw[0]), int(Dw[1]), int(Dw[2]), int(Dw[3])};
             const v4i A1 = {int(Dw[4]), int(Dw[5]), int(Dw[6]), int(Dw[7])};
-            const uint32_t zw = wsel(cur.z, tau);
-            const u4& sv = tau < 2 ? cur.s0 : cur.s1;
+            const uint32_t zw = zw4[tau];
+            const u4& sv = tau < 2 ? ms0 : ms1;
             const uint32_t s01 = wsel(sv, (tau & 1) * 2), s23 = wsel(sv, (tau & 1) * 2 + 1);
-            float sw[4];
-            sw[0] = f16_bits_to_f32(s01 & 0xFFFFu);
-            sw[1] = f16_bits_to_f32(s01 >> 16);
-            sw[2] = f16_bits_to_f32(s23 & 0xFFFFu);
-            sw[3] = f16_bits_to_f32(s23 >> 16);
+            const uint32_t swp[2] = {s01, s23};   // fp16 scale pairs (rows 4q + 0, 1 | 2, 3)
             int zz[4];
 #pragma unroll
             for (int v = 0; v < 4; ++v) zz[v] = int((zw >> (8 * v)) & 0xFFu) - ZOFF;
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const int n = nt * 16 + col;
-                v4i B0 = {0, 0, 0, 0}, B1 = {0, 0, 0, 0};
-                float xsn = 0.0f;
-                int xsumn = 0;
-                if (n < ntok) {
-                    const int8_t* br = bq + n * LDQ + g * GROUP + 16 * q;
-                    B0 = *reinterpret_cast<const v4i*>(br);
-                    B1 = *reinterpret_cast<const v4i*>(br + 64);
-                    xsn = bs[g * NTOK + n];
-                    xsumn = bsum[g * NTOK + n];
-                }
-                v4i C = {-__mul24(zz[0], xsumn), -__mul24(zz[1], xsumn), -__mul24(zz[2], xsumn), -__mul24(zz[3], xsumn)};
+                // an opaque zero offset per tile keeps the compiler from hoisting the B reads of every tile to the
+                // top of the loop (they would not fit in registers)
+                int opaque = 0;
+                asm volatile("" : "+v"(opaque));
+                const int8_t* bqp = bq + opaque;
+                const float* bsp = bs + opaque;
+                const int* bsump = bsum + opaque;
+                const int8_t* br = bqp + n * LDQ + g * GROUP + 16 * q;
+                const v4i B0 = *reinterpret_cast<const v4i*>(br);
+                const v4i B1 = *reinterpret_cast<const v4i*>(br + 64);
+                const float xsn = bsp[g * NTOK + n];
+                const int nxsum = bsump[g * NTOK + n];
+                v4i C = {__mul24(zz[0], nxsum), __mul24(zz[1], nxsum), __mul24(zz[2], nxsum), __mul24(zz[3], nxsum)};
                 C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, C, 0, 0, 0);
                 C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, C, 0, 0, 0);
                 if constexpr (Geo<MODE>::PRODUCTS) {
@@ -191,12 +266,24 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
                     }
                 } else {
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[nt][v] = __builtin_fmaf(sw[v] * xsn, float(C[v]), acc[nt][v]);
+                    for (int v = 0; v < 4; ++v)
+                        acc[nt][v] = __builtin_fmaf(mul_f16_f32(swp[v >> 1], v & 1, xsn), float(C[v]), acc[nt][v]);
                 }
             }
+            // one tile at a time: without this fence the scheduler interleaves every tile of the pass and keeps
+            // all their operands and accumulators live (register pressure, lower occupancy)
+            __builtin_amdgcn_sched_barrier(0);
         }
         if constexpr (!Geo<MODE>::PRODUCTS) {
-            if (sb == NSB - 1) {
+            // superblock partial (an fma chain over its 4 groups) added to the row total in superblock order
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    tot[nt][v] = tot[nt][v] + acc[nt][v];
+                    acc[nt][v] = 0.0f;
+                }
+            if constexpr (sb == NSB - 1) {
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) {
                     const int n = nt * 16 + col;
@@ -204,20 +291,23 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
                         const int slot = it.slot0 + n;
                         if constexpr (MODE == GEMM_GATE_UP) {
                             // lane quad q holds rows gate 8 strip + 2q, up (same), gate + 1, up + 1
-                            const uint32_t z0 = f32_to_f16_bits(silu_f32(acc[nt][0]) * acc[nt][1]);
-                            const uint32_t z1 = f32_to_f16_bits(silu_f32(acc[nt][2]) * acc[nt][3]);
+                            const uint32_t z0 = f32_to_f16_bits(silu_f32(tot[nt][0]) * tot[nt][1]);
+                            const uint32_t z1 = f32_to_f16_bits(silu_f32(tot[nt][2]) * tot[nt][3]);
                             *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
                         } else {
                             const float w = a.slot_weight[slot];
                             *reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q) =
-                                make_float4(w * acc[nt][0], w * acc[nt][1], w * acc[nt][2], w * acc[nt][3]);
+                                make_float4(w * tot[nt][0], w * tot[nt][1], w * tot[nt][2], w * tot[nt][3]);
                         }
                     }
-                    acc[nt][0] = acc[nt][1] = acc[nt][2] = acc[nt][3] = 0.0f;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) tot[nt][v] = 0.0f;
                 }
             }
         }
-    }
+        // refill the slot just consumed with step u + D
+        if constexpr (u + D < NSTEP) load_step<BITS>(mat + size_t(u + D) * SBB, lane, cur);
+    });
 }
 
 template <int MODE, int NT>
@@ -239,7 +329,7 @@ const void* kernel_ptr() { return reinterpret_cast<const void*>(&expert_gemm<MOD
 template <int MODE, int NT>
 hipError_t set_attr() {
     constexpr int K = Geo<MODE>::NSB * SB_K;
-    return hipFuncSetAttribute(kernel_ptr<MODE, NT>(), hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes(16 * NT, K));
+    return hipFuncSetAttribute(kernel_ptr<MODE, NT>(), hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes<MODE, NT>());
 }
 
 template <int MODE, int NT>
@@ -247,7 +337,7 @@ hipError_t launch_t(const GemmArgs& a, int max_items, hipStream_t st) {
     constexpr int K = Geo<MODE>::NSB * SB_K;
     const int rows_per_block = 16 * WAVES * Geo<MODE>::SPW;
     const dim3 grid(a.R / rows_per_block, max_items);
-    expert_gemm<MODE, NT><<<grid, WAVES * 64, lds_bytes(16 * NT, K), st>>>(a);
+    expert_gemm<MODE, NT><<<grid, WAVES * 64, lds_bytes<MODE, NT>(), st>>>(a);
     return hipGetLastError();
 }
 

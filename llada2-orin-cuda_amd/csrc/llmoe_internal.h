@@ -118,6 +118,12 @@ hipError_t launch_combine(const float* Y, const int* tok_slots, int T, int H, in
 hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, int E, float* part, hipStream_t st);
 hipError_t launch_route(const float* part, int nchunks, const float* bias, int T, int E, int K, int C, int block,
                         float rscale, int32_t* topk, float* topw, uint32_t* mask, hipStream_t st);
+// single routing block (T <= block): route + plan + place in one workgroup
+hipError_t launch_route_dispatch(const float* part, int nchunks, const float* bias, int T, int E, int K, int C,
+                                 int block, float rscale, int32_t* topk, float* topw, uint32_t* mask, int has_shared,
+                                 int ntok, const int8_t* bits, int32_t* count, int32_t* start, Item* items,
+                                 int* n_items, int32_t* slot_token, float* slot_weight, int32_t* tok_slots,
+                                 hipStream_t st);
 hipError_t launch_masks(const int32_t* topk, int T, int E, int K, int block, uint32_t* mask, hipStream_t st);
 hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int has_shared, int ntok,
                        int32_t* count, int32_t* start, int32_t* bpre, Item* items, int* n_items, hipStream_t st);

@@ -11,39 +11,45 @@ constexpr int MAXB = 32;    // tokens per routing block (one 32-bit token mask p
 constexpr int MAXE = 256;   // experts (one thread each)
 
 // logits partial c: fma chain over k = c H/8 .. (c+1) H/8 - 1 ascending from 0 (the summation order is fixed so
-// the CPU checker reproduces it). Tile 32 tokens x 64 experts per workgroup, 2 x 4 outputs per thread.
-// grid (E/64, ceil(T/32), 8), 256 threads.
+// the CPU checker reproduces it). Workgroup tile: 32 tokens x 64 experts of one K chunk, the chunk's x and Wr
+// slices staged in LDS by one batch of loads; thread: 2 tokens x 4 experts.
+// grid (E/64, ceil(T/32), 8), 256 threads, dynamic LDS ROUTER_LDS.
+constexpr int RKW = 256;                                          // K per chunk (H = 2048)
+constexpr int ROUTER_LDS = (32 * (RKW + 4) + RKW * 64) * 4;
 __global__ void __launch_bounds__(256) router_logits_kernel(const float* __restrict__ x, const float* __restrict__ Wr,
                                                             int T, int H, int E, float* __restrict__ part) {
-    __shared__ float xs[32][33];
-    __shared__ float ws[32][64];
-    const int e0 = blockIdx.x * 64, t0 = blockIdx.y * 32, c = blockIdx.z, KW = H / ROUTER_KC, kb = c * KW;
+    extern __shared__ __align__(16) float rl[];
+    float* xs = rl;                       // [32][RKW + 4]
+    float* ws = rl + 32 * (RKW + 4);      // [RKW][64]
+    const int e0 = blockIdx.x * 64, t0 = blockIdx.y * 32, c = blockIdx.z, kb = c * RKW;
     const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {                                 // x: 32 x 256 floats as float4
+        const int idx = tid + 256 * i, t = idx >> 6, k4 = idx & 63;
+        const float4 v = t0 + t < T ? *reinterpret_cast<const float4*>(x + size_t(t0 + t) * H + kb + 4 * k4)
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        *reinterpret_cast<float4*>(xs + t * (RKW + 4) + 4 * k4) = v;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {                                // Wr: 256 x 64 floats as float4
+        const int idx = tid + 256 * i, k = idx >> 4, e4 = idx & 15;
+        *reinterpret_cast<float4*>(ws + k * 64 + 4 * e4) =
+            *reinterpret_cast<const float4*>(Wr + size_t(kb + k) * E + e0 + 4 * e4);
+    }
+    __syncthreads();
     float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-    for (int k0 = kb; k0 < kb + KW; k0 += 32) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int idx = tid + 256 * i, t = idx >> 5, k = idx & 31;
-            xs[k][t] = t0 + t < T ? x[size_t(t0 + t) * H + k0 + k] : 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int idx = tid + 256 * i, k = idx >> 6, e = idx & 63;
-            ws[k][e] = Wr[size_t(k0 + k) * E + e0 + e];
-        }
-        __syncthreads();
+    const float* xa = xs + (2 * ty) * (RKW + 4);
+    const float* xb = xa + (RKW + 4);
 #pragma unroll 8
-        for (int kk = 0; kk < 32; ++kk) {
-            const float xa = xs[kk][2 * ty], xb = xs[kk][2 * ty + 1];
-            const float4 w = *reinterpret_cast<const float4*>(&ws[kk][4 * tx]);
-            const float wv[4] = {w.x, w.y, w.z, w.w};
+    for (int k = 0; k < RKW; ++k) {
+        const float a = xa[k], b = xb[k];
+        const float4 w = *reinterpret_cast<const float4*>(ws + k * 64 + 4 * tx);
+        const float wv[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[0][j] = __builtin_fmaf(xa, wv[j], acc[0][j]);
-                acc[1][j] = __builtin_fmaf(xb, wv[j], acc[1][j]);
-            }
+        for (int j = 0; j < 4; ++j) {
+            acc[0][j] = __builtin_fmaf(a, wv[j], acc[0][j]);
+            acc[1][j] = __builtin_fmaf(b, wv[j], acc[1][j]);
         }
-        __syncthreads();
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -56,92 +62,332 @@ __global__ void __launch_bounds__(256) router_logits_kernel(const float* __restr
 
 __device__ __forceinline__ bool beats(float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); }
 
-// One routing block per workgroup, thread = expert (engine/ops.cu:256-327, quant/s03_teacher_pass.py:132-146):
+// Selection keys: (value desc, index asc) as one unsigned 64-bit order: the float's bits mapped to an
+// order-preserving unsigned integer in the high word, 0xFFFF - index in the low word; key 0 = no candidate.
+__device__ __forceinline__ uint64_t sel_key(float v, int idx) {
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (uint64_t(o) << 32) | uint32_t(0xFFFF - idx);
+}
+__device__ __forceinline__ int key_index(uint64_t k) { return 0xFFFF - int(uint32_t(k) & 0xFFFFu); }
+
+__device__ __forceinline__ void cas(uint64_t (&k)[8], int i, int l) {   // afterwards k[i] >= k[l]
+    const uint64_t a = k[i], b = k[l];
+    const bool sw = b > a;
+    k[i] = sw ? b : a;
+    k[l] = sw ? a : b;
+}
+
+// bitonic sorting network on 8 keys, largest first
+__device__ __forceinline__ void sort8(uint64_t (&k)[8]) {
+#pragma unroll
+    for (int s = 2; s <= 8; s <<= 1)
+#pragma unroll
+        for (int j = s >> 1; j > 0; j >>= 1)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int l = i ^ j;
+                if (l > i) {
+                    if ((i & s) == 0) cas(k, i, l);
+                    else cas(k, l, i);
+                }
+            }
+}
+
+// k <- largest 8 of two largest-first sorted lists: max(k[i], w[7 - i]) is bitonic and holds them; a 3-stage
+// bitonic merge sorts it
+__device__ __forceinline__ void merge8(uint64_t (&k)[8], const uint64_t (&w)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) k[i] = w[7 - i] > k[i] ? w[7 - i] : k[i];
+#pragma unroll
+    for (int j = 4; j > 0; j >>= 1)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int l = i ^ j;
+            if (l > i) cas(k, i, l);
+        }
+}
+
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int o) {
+    const uint32_t lo = __shfl_xor(uint32_t(v), o), hi = __shfl_xor(uint32_t(v >> 32), o);
+    return (uint64_t(hi) << 32) | lo;
+}
+
+// exclusive prefix sums of two per-expert values over E <= 256 experts, by wave 0 (4 experts per lane);
+// results in LDS arrays ex_a/ex_b, totals in tot[0..1]. All threads must call it (it synchronises).
+__device__ void expert_scan2(const int* va, const int* vb, int E, int* ex_a, int* ex_b, int* tot) {
+    if (threadIdx.x < 64) {
+        const int l = threadIdx.x;
+        int a[4], b[4], sa = 0, sb = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = 4 * l + j;
+            a[j] = e < E ? va[e] : 0;
+            b[j] = e < E ? vb[e] : 0;
+            sa += a[j];
+            sb += b[j];
+        }
+        int ia = sa, ib = sb;   // inclusive scan over lanes
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int ta = __shfl_up(ia, o), tb2 = __shfl_up(ib, o);
+            if (l >= o) {
+                ia += ta;
+                ib += tb2;
+            }
+        }
+        int ra = ia - sa, rb = ib - sb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = 4 * l + j;
+            if (e < E) {
+                ex_a[e] = ra;
+                ex_b[e] = rb;
+            }
+            ra += a[j];
+            rb += b[j];
+        }
+        if (l == 63) {
+            tot[0] = ia;
+            tot[1] = ib;
+        }
+    }
+    __syncthreads();
+}
+
+// exclusive prefix sum over the NT threads of a block (Hillis-Steele in LDS); *total = the full sum
+template <int NT>
+__device__ int block_excl_scan(int v, int* buf, int* total) {
+    const int i = threadIdx.x;
+    buf[i] = v;
+    __syncthreads();
+    for (int o = 1; o < NT; o <<= 1) {
+        const int add = i >= o ? buf[i - o] : 0;
+        __syncthreads();
+        buf[i] += add;
+        __syncthreads();
+    }
+    const int incl = buf[i];
+    *total = buf[NT - 1];
+    __syncthreads();
+    return incl - v;
+}
+
+// Work-item offsets ordered heaviest first: the shared expert's items, then routed experts by code width
+// (8, 4, 3, 2 bits), expert ascending inside a width -- long workgroups are dispatched first. Wave 0, 4 experts
+// per lane. nit: items per expert (LDS), cls: width class 0..3 per expert (LDS); out: ibase (LDS).
+__device__ void item_offsets_by_width(const int* nit, const int* cls, int E, int shared_items, int* ibase) {
+    if (threadIdx.x < 64) {
+        const int l = threadIdx.x;
+        int base = shared_items;
+        for (int c = 0; c < 4; ++c) {
+            int v[4], sum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = 4 * l + j;
+                v[j] = (e < E && cls[e] == c) ? nit[e] : 0;
+                sum += v[j];
+            }
+            int incl = sum;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int t = __shfl_up(incl, o);
+                if (l >= o) incl += t;
+            }
+            int run = base + incl - sum;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = 4 * l + j;
+                if (e < E && cls[e] == c) ibase[e] = run;
+                run += v[j];
+            }
+            base += __shfl(incl, 63);
+        }
+    }
+    __syncthreads();
+}
+
+struct DispatchOut {         // written by the single-block fused route (decode): the plan + place results
+    int has_shared, ntok;
+    const int8_t* bits;      // code width per expert (orders the work items)
+    int* count;
+    int* start;
+    Item* items;
+    int* n_items;
+    int* slot_token;
+    float* slot_weight;
+    int* tok_slots;
+};
+
+constexpr int RT_THREADS = 1024;
+
+// One routing block per workgroup (engine/ops.cu:256-327, quant/s03_teacher_pass.py:132-146):
 //   logit = sum of the nchunks partials (c ascending); score = sigmoid(logit); s = score + bias;
 //   pool = top-C experts by max over the block's tokens of s, ranked (value desc, index asc) (C >= E: all);
-//   per token top-K of s in the pool, (value desc, index asc), by K rounds of a wavefront arg-max;
-//   w_k = score_k / (sum_k score_k + 1e-20) * rscale.
-// Writes topk/topw [T, K] and mask[block, e] = bit t of the block's tokens that picked e.
-__global__ void __launch_bounds__(256) route_kernel(const float* __restrict__ part, int nchunks,
-                                                    const float* __restrict__ bias, int T, int E, int K, int C,
-                                                    int block, float rscale, int* __restrict__ topk,
-                                                    float* __restrict__ topw, uint32_t* __restrict__ mask) {
-    __shared__ float sig[MAXB][MAXE];
-    __shared__ float key[MAXE];
+//   per token top-K of s in the pool, (value desc, index asc): 8 lanes per token each keep a sorted top-8 of
+//   their 32 experts, then three xor-shuffle merges give every lane the token's top-8;
+//   w_k = score_k / (sum_k score_k + 1e-20) * rscale, the sum in rank order.
+// Writes topk/topw [T, K] and mask[block, e] = bit t of the block's tokens that picked e. FUSED (T <= block, the
+// decode step, engine/ops.cu:333-370): the same workgroup also builds the slots and work items.
+// 1024 threads: every partial of the block is loaded in one batch.
+template <bool FUSED>
+__global__ void __launch_bounds__(RT_THREADS) route_kernel(const float* __restrict__ part, int nchunks,
+                                                           const float* __restrict__ bias, int T, int E, int K, int C,
+                                                           int block, float rscale, int* __restrict__ topk,
+                                                           float* __restrict__ topw, uint32_t* __restrict__ mask,
+                                                           DispatchOut dout) {
+    __shared__ float sig[MAXB][MAXE + 1];
+    __shared__ uint64_t key[MAXE];
     __shared__ float sbias[MAXE];
     __shared__ int inpool[MAXE];
     __shared__ uint32_t tmask[MAXE];
-    const int b = blockIdx.x, t0 = b * block, tb = min(block, T - t0), e = threadIdx.x;
-    if (e < E) {
-        const float be = bias[e];
-        float km = -__builtin_inff();
-        for (int t = 0; t < tb; ++t) {
-            float l = part[size_t(t0 + t) * E + e];
-            for (int c = 1; c < nchunks; ++c) l = l + part[(size_t(c) * T + t0 + t) * E + e];
-            const float sg = sigmoid_f32(l);
-            sig[t][e] = sg;
-            km = fmaxf(km, sg + be);
+    __shared__ int sstart[MAXE];
+    __shared__ int cnt[MAXE];
+    __shared__ int nits[MAXE];
+    __shared__ int ibase[MAXE];
+    __shared__ int tots[2];
+    __shared__ int wcls[MAXE];
+    const int b = blockIdx.x, t0 = b * block, tb = min(block, T - t0), tid = threadIdx.x;
+    if (tid < E) {
+        sbias[tid] = bias[tid];
+        tmask[tid] = 0u;
+    }
+    {   // logits: positions (token, 4 experts), <= 2 per thread, all chunks loaded before any is summed
+        const int E4 = E / 4, npos = tb * E4;
+        float4 p[2][ROUTER_KC];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int pos = tid + r * RT_THREADS, t = pos / E4, e4 = pos % E4;
+#pragma unroll
+            for (int c = 0; c < ROUTER_KC; ++c)
+                if (pos < npos && c < nchunks)
+                    p[r][c] = *reinterpret_cast<const float4*>(part + (size_t(c) * T + t0 + t) * E + 4 * e4);
         }
-        key[e] = km;
-        sbias[e] = be;
-        tmask[e] = 0u;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int pos = tid + r * RT_THREADS, t = pos / E4, e4 = pos % E4;
+            if (pos < npos) {
+                float4 l = p[r][0];
+#pragma unroll
+                for (int c = 1; c < ROUTER_KC; ++c) {
+                    if (c < nchunks) {
+                        l.x = l.x + p[r][c].x;
+                        l.y = l.y + p[r][c].y;
+                        l.z = l.z + p[r][c].z;
+                        l.w = l.w + p[r][c].w;
+                    }
+                }
+                sig[t][4 * e4] = sigmoid_f32(l.x);
+                sig[t][4 * e4 + 1] = sigmoid_f32(l.y);
+                sig[t][4 * e4 + 2] = sigmoid_f32(l.z);
+                sig[t][4 * e4 + 3] = sigmoid_f32(l.w);
+            }
+        }
     }
     __syncthreads();
-    if (e < E) {
+    if (C < E) {
+        if (tid < E) {
+            float km = -__builtin_inff();
+            for (int t = 0; t < tb; ++t) km = fmaxf(km, sig[t][tid] + sbias[tid]);
+            key[tid] = sel_key(km, tid);
+        }
+        __syncthreads();
+    }
+    if (tid < E) {   // pool = the C largest keys: rank = number of larger keys
         int rank = 0;
         if (C < E) {
-            const float ke = key[e];
-            for (int j = 0; j < E; ++j) rank += beats(key[j], j, ke, e);
+            const uint64_t ke = key[tid];
+#pragma unroll 8
+            for (int j = 0; j < E; ++j) rank += key[j] > ke;
         }
-        inpool[e] = rank < C;
+        inpool[tid] = rank < C;
     }
     __syncthreads();
-    const int lane = e & 63, wave = e >> 6;
-    for (int t = wave; t < tb; t += 4) {
-        float v[4];
+    // selection: 32 lanes per token (all 1024 threads), 8 candidates per lane read before use and sorted, then
+    // five xor-shuffle merges (1 .. 16) give every lane of the token its best 8
+    const int tl = tid >> 5, sub = tid & 31;
+    uint64_t best[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int ex = lane + 64 * j;
-            v[j] = (ex < E && inpool[ex]) ? sig[t][ex] + sbias[ex] : -__builtin_inff();
-        }
-        int taken = 0, mysel = -1;
-        float mysig = 0.0f, wsum = 0.0f;
-        for (int k = 0; k < K; ++k) {
-            float bv = -__builtin_inff();
-            int bi = 0x7fffffff;
+    for (int j = 0; j < 8; ++j) {
+        const int ex = sub * 8 + j;
+        const bool ok = tl < tb && ex < E && inpool[ex];
+        best[j] = ok ? sel_key(sig[tl][ex] + sbias[ex], ex) : 0ull;
+    }
+    sort8(best);
+#pragma unroll 1
+    for (int o = 1; o < 32; o <<= 1) {
+        uint64_t other[8];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int ex = lane + 64 * j;
-                if (!((taken >> j) & 1) && ex < E && beats(v[j], ex, bv, bi)) {
-                    bv = v[j];
-                    bi = ex;
+        for (int k = 0; k < 8; ++k) other[k] = shfl_xor64(best[k], o);
+        merge8(best, other);
+    }
+    int bi[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) bi[k] = key_index(best[k]);
+    float mine = 0.0f, wsum = 0.0f;
+    int mysel = 0;
+    const bool owner = tl < tb && sub < K;
+    if (tl < tb) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (k < K) {
+                const float sk = sig[tl][bi[k]];
+                wsum = wsum + sk;
+                if (k == sub) {
+                    mine = sk;
+                    mysel = bi[k];
                 }
             }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o);
-                const int oi = __shfl_xor(bi, o);
-                if (beats(ov, oi, bv, bi)) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
-            if ((bi & 63) == lane) taken |= 1 << (bi >> 6);
-            const float sk = sig[t][bi];
-            wsum = wsum + sk;
-            if (lane == k) {
-                mysel = bi;
-                mysig = sk;
-            }
         }
-        if (lane < K) {
-            topk[size_t(t0 + t) * K + lane] = mysel;
-            topw[size_t(t0 + t) * K + lane] = mysig / (wsum + 1e-20f) * rscale;
-            atomicOr(&tmask[mysel], 1u << t);
+        if (owner) {
+            topk[size_t(t0 + tl) * K + sub] = mysel;
+            topw[size_t(t0 + tl) * K + sub] = mine / (wsum + 1e-20f) * rscale;
+            atomicOr(&tmask[mysel], 1u << tl);
         }
     }
     __syncthreads();
-    if (e < E) mask[size_t(b) * E + e] = tmask[e];
+    if (tid < E) mask[size_t(b) * E + tid] = tmask[tid];
+    if constexpr (FUSED) {
+        // one block: slot ranges = exclusive scan of the per-expert token counts; items of <= ntok slots, the
+        // item list ordered heaviest first (shared expert, then 8 / 4 / 3 / 2-bit experts)
+        const int ns = dout.has_shared ? (T + dout.ntok - 1) / dout.ntok : 0;
+        if (tid < E) {
+            const int c = __popc(tmask[tid]);
+            cnt[tid] = c;
+            nits[tid] = (c + dout.ntok - 1) / dout.ntok;
+            const int b = dout.bits[tid];
+            wcls[tid] = b == 8 ? 0 : b == 4 ? 1 : b == 3 ? 2 : 3;
+        }
+        __syncthreads();
+        expert_scan2(cnt, nits, E, sstart, ibase, tots);
+        item_offsets_by_width(nits, wcls, E, ns, ibase);
+        const int tot_items = tots[1];
+        if (tid < E) {
+            const int c = cnt[tid], st = sstart[tid], ib = ibase[tid], nit = nits[tid];
+            dout.count[tid] = c;
+            dout.start[tid] = st;
+            for (int j = 0; j < nit; ++j)
+                dout.items[ib + j] = Item{tid, st + j * dout.ntok, min(dout.ntok, c - j * dout.ntok), 0};
+        }
+        if (tid < ns) dout.items[tid] = Item{E, T * K + tid * dout.ntok, min(dout.ntok, T - tid * dout.ntok), 0};
+        if (tid == 0) *dout.n_items = tot_items + ns;
+        __syncthreads();
+        if (owner) {
+            const int t = t0 + tl;
+            const int sl = sstart[mysel] + __popc(tmask[mysel] & ((1u << tl) - 1u));
+            dout.slot_token[sl] = t;
+            dout.slot_weight[sl] = mine / (wsum + 1e-20f) * rscale;
+            dout.tok_slots[size_t(t) * (K + 1) + sub] = sl;
+        }
+        if (tid < tb) {
+            const int t = t0 + tid;
+            if (dout.has_shared) {
+                dout.slot_token[T * K + t] = t;
+                dout.slot_weight[T * K + t] = 1.0f;
+            }
+            dout.tok_slots[size_t(t) * (K + 1) + K] = dout.has_shared ? T * K + t : -1;
+        }
+    }
 }
 
 // Token masks of externally given routing. grid nb, 256 threads.
@@ -159,23 +405,6 @@ __global__ void __launch_bounds__(256) masks_kernel(const int* __restrict__ topk
     if (threadIdx.x < E) mask[size_t(b) * E + threadIdx.x] = tmask[threadIdx.x];
 }
 
-// exclusive prefix sum over the 256 threads of a block (Hillis-Steele in LDS); *total = the full sum
-__device__ int block_excl_scan(int v, int* buf, int* total) {
-    const int i = threadIdx.x;
-    buf[i] = v;
-    __syncthreads();
-    for (int o = 1; o < 256; o <<= 1) {
-        const int add = i >= o ? buf[i - o] : 0;
-        __syncthreads();
-        buf[i] += add;
-        __syncthreads();
-    }
-    const int incl = buf[i];
-    *total = buf[255];
-    __syncthreads();
-    return incl - v;
-}
-
 // Slot ranges and work items (engine/ops.cu:333-370, :384-410): slots expert-major (expert ascending), inside
 // an expert block-major then token-ascending; items of <= ntok slots per expert; shared-expert items last.
 // One workgroup, thread = expert.
@@ -189,9 +418,9 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     if (e < E)
         for (int b = 0; b < nb; ++b) c += __popc(mask[size_t(b) * E + e]);
     int tot_slots, tot_items;
-    const int st = block_excl_scan(c, buf, &tot_slots);
+    const int st = block_excl_scan<256>(c, buf, &tot_slots);
     const int nit = e < E ? (c + ntok - 1) / ntok : 0;
-    const int ib = block_excl_scan(nit, buf, &tot_items);
+    const int ib = block_excl_scan<256>(nit, buf, &tot_items);
     if (e < E) {
         count[e] = c;
         start[e] = st;
@@ -240,15 +469,34 @@ __global__ void __launch_bounds__(256) place_kernel(const int* __restrict__ topk
 }  // namespace
 
 hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, int E, float* part, hipStream_t st) {
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(router_logits_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, ROUTER_LDS);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
     const dim3 grid(E / 64, (T + 31) / 32, ROUTER_KC);
-    router_logits_kernel<<<grid, 256, 0, st>>>(x, Wr, T, H, E, part);
+    router_logits_kernel<<<grid, 256, ROUTER_LDS, st>>>(x, Wr, T, H, E, part);
     return hipGetLastError();
 }
 
 hipError_t launch_route(const float* part, int nchunks, const float* bias, int T, int E, int K, int C, int block,
                         float rscale, int32_t* topk, float* topw, uint32_t* mask, hipStream_t st) {
     const int nb = (T + block - 1) / block;
-    route_kernel<<<nb, 256, 0, st>>>(part, nchunks, bias, T, E, K, C, block, rscale, topk, topw, mask);
+    route_kernel<false><<<nb, RT_THREADS, 0, st>>>(part, nchunks, bias, T, E, K, C, block, rscale, topk, topw, mask,
+                                                   DispatchOut{});
+    return hipGetLastError();
+}
+
+hipError_t launch_route_dispatch(const float* part, int nchunks, const float* bias, int T, int E, int K, int C,
+                                 int block, float rscale, int32_t* topk, float* topw, uint32_t* mask, int has_shared,
+                                 int ntok, const int8_t* bits, int32_t* count, int32_t* start, Item* items,
+                                 int* n_items, int32_t* slot_token, float* slot_weight, int32_t* tok_slots,
+                                 hipStream_t st) {
+    if (T > block) return hipErrorInvalidValue;
+    const DispatchOut d{has_shared, ntok, bits, count, start, items, n_items, slot_token, slot_weight, tok_slots};
+    route_kernel<true><<<1, RT_THREADS, 0, st>>>(part, nchunks, bias, T, E, K, C, block, rscale, topk, topw, mask, d);
     return hipGetLastError();
 }
 

@@ -58,8 +58,11 @@ class Buffers(ctypes.Structure):
 EXPORTS = [
     "llmoe_layer_create", "llmoe_layer_destroy", "llmoe_quantize_a8", "llmoe_route", "llmoe_dispatch",
     "llmoe_experts", "llmoe_layer_forward", "llmoe_layer_buffers", "llmoe_layer_weight_bytes",
-    "llmoe_group_products", "llmoe_last_error",
+    "llmoe_group_products", "llmoe_layer_set_profiling", "llmoe_layer_stage_ms", "llmoe_layer_time_stage", "llmoe_layers_time_stage",
+    "llmoe_last_error",
 ]
+
+STAGES = ["quant", "router", "route", "dispatch", "gate_up", "fwht", "down", "combine"]
 
 _lib = None
 
@@ -86,6 +89,10 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.llmoe_layer_buffers.argtypes = [vp, ctypes.POINTER(Buffers)]
     lib.llmoe_layer_weight_bytes.argtypes = [vp, ctypes.POINTER(sz)]
     lib.llmoe_group_products.argtypes = [vp, i, i, vp, vp, i, vp, vp]
+    lib.llmoe_layer_set_profiling.argtypes = [vp, i]
+    lib.llmoe_layer_stage_ms.argtypes = [vp, ctypes.POINTER(ctypes.c_float)]
+    lib.llmoe_layer_time_stage.argtypes = [vp, i, i, vp, ctypes.POINTER(ctypes.c_float)]
+    lib.llmoe_layers_time_stage.argtypes = [ctypes.POINTER(ctypes.c_void_p), i, i, i, vp, ctypes.POINTER(ctypes.c_float)]
     for name in EXPORTS:
         if name != "llmoe_last_error":
             getattr(lib, name).restype = ctypes.c_int
@@ -184,6 +191,22 @@ class Layer:
                                              _stream(stream)))
         return P
 
+    def set_profiling(self, on: bool) -> None:
+        _check(self.lib.llmoe_layer_set_profiling(self.handle, int(on)))
+
+    def stage_ms(self) -> dict:
+        """Per-stage milliseconds of the latest profiled call (stages not run: absent)."""
+        arr = (ctypes.c_float * len(STAGES))()
+        _check(self.lib.llmoe_layer_stage_ms(self.handle, arr))
+        return {n: float(v) for n, v in zip(STAGES, arr) if v >= 0}
+
+    def time_stage(self, stage: str, reps: int = 50, stream=None) -> float:
+        """Average ms of one expert stage of the latest call, re-launched `reps` times back to back."""
+        v = ctypes.c_float()
+        _check(self.lib.llmoe_layer_time_stage(self.handle, STAGES.index(stage), reps, _stream(stream),
+                                               ctypes.byref(v)))
+        return float(v.value)
+
     def buffers(self) -> Buffers:
         b = Buffers()
         _check(self.lib.llmoe_layer_buffers(self.handle, ctypes.byref(b)))
@@ -203,6 +226,15 @@ class Layer:
         out = np.empty(shape, dtype=dtype)
         _hip_memcpy_d2h(out, ptr, n)
         return out
+
+
+def time_stage_layers(layers, stage: str, reps: int = 20, stream=None) -> float:
+    """Average ms per launch of one expert stage, re-launched over several layers in turn (llmoe_layers_time_stage)."""
+    lib = load_library()
+    arr = (ctypes.c_void_p * len(layers))(*[L.handle.value for L in layers])
+    v = ctypes.c_float()
+    _check(lib.llmoe_layers_time_stage(arr, len(layers), STAGES.index(stage), reps, _stream(stream), ctypes.byref(v)))
+    return float(v.value)
 
 
 _hip = None

@@ -21,6 +21,8 @@ HIPCC_FLAGS = [
     # no packed-fp32 instructions (v_pk_*_f32) anywhere in this library
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
+    # MFMA accumulators in VGPRs (no accvgpr copies around every MFMA)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 
@@ -29,7 +31,7 @@ def build_library(verbose: bool = False) -> Path:
     out = PKG / "libllmoe.so"
     tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc, *HIPCC_FLAGS, f"-I{ROOT / 'include'}", f"-I{CSRC}", *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
-    r = subprocess.run(cmd, capture_output=True, text=True)
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("hipcc failed building libllmoe.so")

@@ -353,13 +353,19 @@ void orc_group_products(const uint8_t* codes, const uint8_t* zero, int R, int K,
         }
 }
 
-/* fp32 epilogue of one row, engine/moe_i8.cu:377-383: acc = 0; per group g ascending
- *   acc = fma(scale_w[r, g] * scale_x[g], float(P[r, g]), acc)
- * (the reference adds the product with a separate rounding; this build fuses it, identically on CPU and GPU). */
+/* fp32 epilogue of one row, engine/moe_i8.cu:377-383, which accumulates sum_g scale_w * scale_x * P_g in group
+ * order. This build fixes the order as: per superblock of 4 groups (512 columns) an fma chain from 0,
+ *   part_b = fma(scale_w[r, g] * scale_x[g], float(P[r, g]), part_b)     g = 4b .. 4b + 3 ascending
+ * and the superblock partials added in order, total = ((0 + part_0) + part_1) + ... -- the same operation
+ * sequence on CPU and GPU (the GPU computes the superblocks of a row in different waves). */
 static inline float row_epilogue(const int32_t* P, const uint16_t* sw, const float* sx, int G) {
-    float acc = 0.0f;
-    for (int g = 0; g < G; ++g) acc = fmaf(orc_f16_to_f32(sw[g]) * sx[g], (float)P[g], acc);
-    return acc;
+    float total = 0.0f;
+    for (int b = 0; b < G / 4; ++b) {
+        float part = 0.0f;
+        for (int g = 4 * b; g < 4 * b + 4; ++g) part = fmaf(orc_f16_to_f32(sw[g]) * sx[g], (float)P[g], part);
+        total = total + part;
+    }
+    return total;
 }
 
 /* FWHT-512 in fp32, Sylvester order: stages h = 1, 2, ..., 256, butterfly (a, b) -> (a + b, a - b) on indices
