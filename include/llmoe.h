@@ -103,7 +103,8 @@ typedef struct {
     int32_t* count; int32_t* start;                    /* slots per routed expert      [E] */
     int32_t* slot_token; float* slot_weight;           /*                              [S] */
     int32_t* tok_slots;                                /* [T, K + 1] (last: shared slot, -1 if none) */
-    int32_t* items; int32_t* n_items;                  /* work items {expert, slot0, ntok, 0} */
+    int32_t* items; int32_t* n_items;                  /* gate_up work units {expert, slot0, ntok, row block};
+                                                          n_items[0] / [1]: gate_up / down unit counts */
     uint16_t* Z;                                       /* fp16 SiLU(g) u               [S, I] */
     int8_t* zq; float* zs; int32_t* zsum;              /* A8(Z H512)                   [S, I], [S, I/128] */
     float* Y;                                          /* weighted expert outputs      [S, H] */

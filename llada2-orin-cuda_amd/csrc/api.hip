@@ -64,13 +64,13 @@ struct llmoe_layer {
     int32_t* topk = nullptr; float* topw = nullptr;
     uint32_t* mask = nullptr; int32_t* bpre = nullptr;
     int32_t* count = nullptr; int32_t* start = nullptr;
-    Item* items = nullptr; int* n_items = nullptr;
+    Item* units_gu = nullptr; Item* units_dn = nullptr; int* n_units = nullptr;   // GEMM work units
     int32_t* slot_token = nullptr; float* slot_weight = nullptr; int32_t* tok_slots = nullptr;
     uint16_t* Z = nullptr; int8_t* zq = nullptr; float* zs = nullptr; int32_t* zsum = nullptr;
     float* Y = nullptr;
-    Item* p_item = nullptr; int* p_count = nullptr;  // single-item list of llmoe_group_products
-    Item p_item_host{}; int p_count_host = 1;
-    size_t items_cap = 0;
+    Item* p_item = nullptr; int* p_count = nullptr;  // unit list of llmoe_group_products
+    Item p_item_host[MAX_UNITS_PER_ITEM] = {}; int p_count_host = 1;
+    size_t items_cap = 0;                           // work items (before the split into row blocks)
     // routing state
     int routed_T = -1, ntok = 16, max_items = 0;
     // stage timing
@@ -142,8 +142,8 @@ int plan_and_place(llmoe_layer* L, const int32_t* topk, const float* topw, int T
     choose_items(L, T);
     if (size_t(L->max_items) > L->items_cap) return fail(LLMOE_EINVAL, "item capacity exceeded");
     L->mark(LLMOE_STAGE_DISPATCH, false, st);
-    HIPCHECK(launch_plan(L->mask, T, d.n_experts, d.top_k, d.block, d.has_shared, L->ntok, L->count, L->start, L->bpre,
-                         L->items, L->n_items, st));
+    HIPCHECK(launch_plan(L->mask, T, d.n_experts, d.top_k, d.block, d.has_shared, L->ntok, L->bits_d, L->count,
+                         L->start, L->bpre, L->units_gu, L->units_dn, L->n_units, st));
     HIPCHECK(launch_place(topk, topw, L->mask, L->bpre, T, d.n_experts, d.top_k, d.block, d.has_shared,
                           L->slot_token, L->slot_weight, L->tok_slots, st));
     L->mark(LLMOE_STAGE_DISPATCH, true, st);
@@ -260,8 +260,9 @@ int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t bl
     ALLOC(L->count, E);
     ALLOC(L->start, E);
     L->items_cap = E + (Tm * K + 15) / 16 + (Tm + 15) / 16 + 2;
-    ALLOC(L->items, L->items_cap);
-    ALLOC(L->n_items, 1);
+    ALLOC(L->units_gu, L->items_cap * MAX_UNITS_PER_ITEM);
+    ALLOC(L->units_dn, L->items_cap * MAX_UNITS_PER_ITEM);
+    ALLOC(L->n_units, 2);
     ALLOC(L->slot_token, S);
     ALLOC(L->slot_weight, S);
     ALLOC(L->tok_slots, Tm * (K + 1));
@@ -270,7 +271,7 @@ int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t bl
     ALLOC(L->zs, S * (I / GROUP));
     ALLOC(L->zsum, S * (I / GROUP));
     ALLOC(L->Y, S * H);
-    ALLOC(L->p_item, 1);
+    ALLOC(L->p_item, MAX_UNITS_PER_ITEM);
     ALLOC(L->p_count, 1);
 #undef ALLOC
     *out = L;
@@ -316,8 +317,8 @@ int llmoe_route(llmoe_layer* L, const float* x, const float* logits, int T, llmo
         if (size_t(L->max_items) > L->items_cap) return fail(LLMOE_EINVAL, "item capacity exceeded");
         HIPCHECK(launch_route_dispatch(part, nchunks, L->bias, T, d.n_experts, d.top_k, d.pool, d.block,
                                        d.routed_scale, L->topk, L->topw, L->mask, d.has_shared, L->ntok, L->bits_d,
-                                       L->count, L->start, L->items, L->n_items, L->slot_token, L->slot_weight,
-                                       L->tok_slots, st));
+                                       L->count, L->start, L->units_gu, L->units_dn, L->n_units, L->slot_token,
+                                       L->slot_weight, L->tok_slots, st));
         L->mark(LLMOE_STAGE_ROUTE, true, st);
         L->routed_T = T;
         return LLMOE_OK;
@@ -354,10 +355,10 @@ int llmoe_experts(llmoe_layer* L, const int8_t* xq, const float* xs, const int32
     GemmArgs g{};
     g.base = L->arena;
     g.bits = L->bits_d;
-    g.items = L->items;
-    g.n_items = L->n_items;
     g.slot_weight = L->slot_weight;
     // gate_up: B rows are token rows of x'
+    g.items = L->units_gu;
+    g.n_items = L->n_units;
     g.off = L->gu_off_d;
     g.slot_token = L->slot_token;
     g.xq = xq; g.xs = xs; g.xsum = xsum;
@@ -370,6 +371,8 @@ int llmoe_experts(llmoe_layer* L, const int8_t* xq, const float* xs, const int32
     HIPCHECK(launch_fwht_a8(L->Z, S, L->zq, L->zs, L->zsum, st));
     L->mark(LLMOE_STAGE_FWHT, true, st);
     // down: B rows are slot rows of Z'
+    g.items = L->units_dn;
+    g.n_items = L->n_units + 1;
     g.off = L->d_off_d;
     g.slot_token = nullptr;
     g.xq = L->zq; g.xs = L->zs; g.xsum = L->zsum;
@@ -474,7 +477,7 @@ int llmoe_layer_buffers(const llmoe_layer* L, llmoe_buffers* o) {
     o->topk = L->topk; o->topw = L->topw;
     o->count = L->count; o->start = L->start;
     o->slot_token = L->slot_token; o->slot_weight = L->slot_weight; o->tok_slots = L->tok_slots;
-    o->items = reinterpret_cast<int32_t*>(L->items); o->n_items = L->n_items;
+    o->items = reinterpret_cast<int32_t*>(L->units_gu); o->n_items = L->n_units;
     o->Z = L->Z; o->zq = L->zq; o->zs = L->zs; o->zsum = L->zsum; o->Y = L->Y;
     o->ntok = L->ntok; o->max_items = L->max_items;
     return LLMOE_OK;
@@ -495,8 +498,12 @@ int llmoe_group_products(llmoe_layer* L, int expert, int which, const int8_t* xq
     if (which != 0 && which != 1) return fail(LLMOE_EINVAL, "which = %d", which);
     if (n < 1 || n > 64) return fail(LLMOE_EINVAL, "n = %d outside [1, 64]", n);
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    L->p_item_host = Item{expert, 0, n, 0};
-    HIPCHECK(hipMemcpyAsync(L->p_item, &L->p_item_host, sizeof(Item), hipMemcpyHostToDevice, st));
+    int b8 = 0;
+    HIPCHECK(hipMemcpy(&b8, L->bits_d + expert, 1, hipMemcpyDeviceToHost));
+    const int nrb = gemm_row_blocks(which == 1, int(int8_t(b8)));
+    for (int r = 0; r < nrb; ++r) L->p_item_host[r] = Item{expert, 0, n, r};
+    L->p_count_host = nrb;
+    HIPCHECK(hipMemcpyAsync(L->p_item, L->p_item_host, nrb * sizeof(Item), hipMemcpyHostToDevice, st));
     HIPCHECK(hipMemcpyAsync(L->p_count, &L->p_count_host, sizeof(int), hipMemcpyHostToDevice, st));
     GemmArgs g{};
     g.base = L->arena;

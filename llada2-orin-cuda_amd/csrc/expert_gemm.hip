@@ -10,9 +10,9 @@
 // once per item): grid (row blocks, items); a workgroup = 4 waves; wave w owns SPW consecutive 16-row strips and
 // streams them through a register ring (dwordx4 loads, 1 KiB contiguous per wave and load). The item's B rows
 // (int8 activations + per-group scales and sums) are staged once per workgroup in LDS.
-//   gate_up (MODE 0): rows 2I = 1024, K = H = 2048, SPW 1; out Z[slot, i] = fp16(SiLU(g_i) u_i)
+//   gate_up (MODE 0): rows 2I = 1024, K = H = 2048; out Z[slot, i] = fp16(SiLU(g_i) u_i)
 //                     (engine/moe_i8.cu:219-221)
-//   down    (MODE 1): rows H = 2048, K = I = 512, SPW 4;  out Y[slot, h] = w_slot acc (engine/moe_i8.cu:222-231)
+//   down    (MODE 1): rows H = 2048, K = I = 512; out Y[slot, h] = w_slot acc (engine/moe_i8.cu:222-231)
 //   products (MODE 2, 3): raw P_g per (token, row, group) in either geometry, for the bit-exactness test.
 #include <type_traits>
 
@@ -25,7 +25,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 
-constexpr int WAVES = 4;
+constexpr int WAVES = GEMM_WAVES;
 
 template <int I, int N, class F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -103,7 +103,11 @@ struct Geo {
     static constexpr bool DOWN_SHAPE = MODE == GEMM_DOWN || MODE == GEMM_PRODUCTS_DOWN;
     static constexpr bool PRODUCTS = MODE == GEMM_PRODUCTS_GATE_UP || MODE == GEMM_PRODUCTS_DOWN;
     static constexpr int NSB = DOWN_SHAPE ? 1 : 4;       // K = 512 or 2048
-    static constexpr int SPW = DOWN_SHAPE ? 8 : 4;       // strips per wave, streamed as one ring
+    // strips per wave (streamed as one ring) by code width, so that every wave streams about the same bytes
+    // (~35 KB): the workgroups of wide codes would otherwise be the tail of the launch
+    template <int BITS>
+    static constexpr int spw() { return gemm_spw(DOWN_SHAPE, BITS); }
+    static constexpr int SPW_MAX = spw<2>();
 };
 
 // ring depth (superblock steps in flight per wave), a divisor of 4. Registers hold only code bytes (the
@@ -117,18 +121,20 @@ struct Ring {
 // superblocks [strip][superblock][192 B]
 __host__ __device__ constexpr int b_bytes(int ntok, int K) { return ntok * (K + 16) + ntok * (K / GROUP) * 8; }
 template <int MODE>
-__host__ __device__ constexpr int meta_bytes() { return WAVES * Geo<MODE>::SPW * Geo<MODE>::NSB * META_SB; }
+__host__ __device__ constexpr int meta_bytes() { return WAVES * Geo<MODE>::SPW_MAX * Geo<MODE>::NSB * META_SB; }
 template <int MODE, int NT>
 __host__ __device__ constexpr int lds_bytes() { return b_bytes(16 * NT, Geo<MODE>::NSB * SB_K) + meta_bytes<MODE>(); }
 
 template <int BITS, int MODE, int NT>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uint8_t* lds, int row_block) {
-    constexpr int NSB = Geo<MODE>::NSB, SPW = Geo<MODE>::SPW, NSTEP = NSB * SPW, D = Ring<BITS>::D;
+    constexpr int NSB = Geo<MODE>::NSB, SPW = Geo<MODE>::template spw<BITS>(), NSTEP = NSB * SPW;
+    constexpr int D = Ring<BITS>::D < NSTEP ? Ring<BITS>::D : NSTEP;
     static_assert(NSTEP % 4 == 0 && 4 % D == 0, "ring geometry");
     constexpr int K = NSB * SB_K, G = K / GROUP, NTOK = 16 * NT, LDQ = K + 16;
     constexpr size_t SBB = sb_bytes(BITS);
     constexpr int ZOFF = BITS == 8 ? 128 : 0;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, col = lane & 15;
+    if ((row_block + 1) * WAVES * SPW * 16 > a.R) return;    // not a row block of this code width
     const int strip0 = (row_block * WAVES + wave) * SPW;
     const uint8_t* mat = a.base + a.off[it.expert] + size_t(strip0) * NSB * SBB;
 
@@ -205,6 +211,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
     }
     __syncthreads();
 
+    // routing weights of this lane's slots, read before the stream: a load inside the ring would make the
+    // compiler wait for every outstanding weight load
+    float wts[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int n = nt * 16 + col;
+        wts[nt] = (MODE == GEMM_DOWN && n < ntok) ? a.slot_weight[it.slot0 + n] : 0.0f;
+    }
     float acc[NT][4], tot[NT][4];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
@@ -240,18 +254,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const int n = nt * 16 + col;
-                // an opaque zero offset per tile keeps the compiler from hoisting the B reads of every tile to the
-                // top of the loop (they would not fit in registers)
-                int opaque = 0;
-                asm volatile("" : "+v"(opaque));
-                const int8_t* bqp = bq + opaque;
-                const float* bsp = bs + opaque;
-                const int* bsump = bsum + opaque;
-                const int8_t* br = bqp + n * LDQ + g * GROUP + 16 * q;
+                const int8_t* br = bq + n * LDQ + g * GROUP + 16 * q;
                 const v4i B0 = *reinterpret_cast<const v4i*>(br);
                 const v4i B1 = *reinterpret_cast<const v4i*>(br + 64);
-                const float xsn = bsp[g * NTOK + n];
-                const int nxsum = bsump[g * NTOK + n];
+                const float xsn = bs[g * NTOK + n];
+                const int nxsum = bsum[g * NTOK + n];
                 v4i C = {__mul24(zz[0], nxsum), __mul24(zz[1], nxsum), __mul24(zz[2], nxsum), __mul24(zz[3], nxsum)};
                 C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, C, 0, 0, 0);
                 C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, C, 0, 0, 0);
@@ -270,8 +277,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
                         acc[nt][v] = __builtin_fmaf(mul_f16_f32(swp[v >> 1], v & 1, xsn), float(C[v]), acc[nt][v]);
                 }
             }
-            // one tile at a time: without this fence the scheduler interleaves every tile of the pass and keeps
-            // all their operands and accumulators live (register pressure, lower occupancy)
+            // one tile at a time: the accumulators are materialised here, otherwise the compiler defers each
+            // tile's fp32 accumulation (a serial fma chain) to the strip end and keeps every tile's results live
+            if constexpr (!Geo<MODE>::PRODUCTS) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    asm volatile("" : "+v"(acc[nt][0]), "+v"(acc[nt][1]), "+v"(acc[nt][2]), "+v"(acc[nt][3]));
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
         if constexpr (!Geo<MODE>::PRODUCTS) {
@@ -295,7 +307,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
                             const uint32_t z1 = f32_to_f16_bits(silu_f32(tot[nt][2]) * tot[nt][3]);
                             *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
                         } else {
-                            const float w = a.slot_weight[slot];
+                            const float w = wts[nt];
                             *reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q) =
                                 make_float4(w * tot[nt][0], w * tot[nt][1], w * tot[nt][2], w * tot[nt][3]);
                         }
@@ -310,17 +322,21 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
     });
 }
 
+// Persistent: the grid is the number of workgroups that fit the GPU at once; each workgroup takes the work units
+// blockIdx.x, blockIdx.x + gridDim.x, ... (units are ordered heaviest first, so the long ones start first).
 template <int MODE, int NT>
 __global__ void __launch_bounds__(WAVES * 64) expert_gemm(GemmArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const int item = blockIdx.y;
-    if (item >= *a.n_items) return;
-    const Item it = a.items[item];
-    const int bits = a.bits[it.expert];
-    if (bits == 2) gemm_body<2, MODE, NT>(a, it, lds, blockIdx.x);
-    else if (bits == 3) gemm_body<3, MODE, NT>(a, it, lds, blockIdx.x);
-    else if (bits == 4) gemm_body<4, MODE, NT>(a, it, lds, blockIdx.x);
-    else gemm_body<8, MODE, NT>(a, it, lds, blockIdx.x);
+    const int n = *a.n_items;
+    for (int u = blockIdx.x; u < n; u += gridDim.x) {
+        const Item it = a.items[u];
+        const int bits = a.bits[it.expert];
+        if (bits == 2) gemm_body<2, MODE, NT>(a, it, lds, it.rb);
+        else if (bits == 3) gemm_body<3, MODE, NT>(a, it, lds, it.rb);
+        else if (bits == 4) gemm_body<4, MODE, NT>(a, it, lds, it.rb);
+        else gemm_body<8, MODE, NT>(a, it, lds, it.rb);
+        __syncthreads();   // the next unit re-stages the LDS
+    }
 }
 
 template <int MODE, int NT>
@@ -333,10 +349,18 @@ hipError_t set_attr() {
 }
 
 template <int MODE, int NT>
-hipError_t launch_t(const GemmArgs& a, int max_items, hipStream_t st) {
-    constexpr int K = Geo<MODE>::NSB * SB_K;
-    const int rows_per_block = 16 * WAVES * Geo<MODE>::SPW;
-    const dim3 grid(a.R / rows_per_block, max_items);
+hipError_t launch_t(const GemmArgs& a, int, hipStream_t st) {
+    static int grid = 0;
+    if (!grid) {   // workgroups resident at once on the whole GPU
+        int dev = 0, cus = 0, per_cu = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e == hipSuccess)
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel_ptr<MODE, NT>(), WAVES * 64,
+                                                             lds_bytes<MODE, NT>());
+        if (e != hipSuccess) return e;
+        grid = cus * (per_cu > 0 ? per_cu : 1);
+    }
     expert_gemm<MODE, NT><<<grid, WAVES * 64, lds_bytes<MODE, NT>(), st>>>(a);
     return hipGetLastError();
 }

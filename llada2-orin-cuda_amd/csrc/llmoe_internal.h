@@ -12,13 +12,27 @@ constexpr int SB_K = 512;        // K columns per superblock = 4 groups
 constexpr int META_SB = 192;     // per strip and superblock: 64 fp16 scales + 64 u8 zeros
 constexpr int ROUTER_KC = 8;     // router K chunks (fixed summation order)
 
-// One work item of the expert GEMMs: `ntok` consecutive slots of one expert.
+// One work unit of the expert GEMMs: `ntok` consecutive slots of one expert, row block `rb` of its matrix.
 struct Item {
     int expert;
     int slot0;
     int ntok;
-    int pad;
+    int rb;
 };
+
+// GEMM geometry shared by the dispatch kernels (which emit the work units) and the GEMM kernels: a workgroup of
+// GEMM_WAVES waves covers 16 * GEMM_WAVES * spw rows, spw = strips per wave chosen by code width so that every
+// wave streams about the same bytes (2-bit codes: 4 strips of gate_up, 3/4-bit: 2, 8-bit: 1; down has K/4 and
+// four times the strips).
+constexpr int GEMM_WAVES = 4;
+__host__ __device__ constexpr int gemm_spw(bool down, int bits) {
+    return (down ? 4 : 1) * (bits == 2 ? 4 : bits == 8 ? 1 : 2);
+}
+// row blocks (work units per work item) of a gate_up [2I = 1024] or down [H = 2048] matrix
+__host__ __device__ constexpr int gemm_row_blocks(bool down, int bits) {
+    return (down ? 2048 : 1024) / (16 * GEMM_WAVES * gemm_spw(down, bits));
+}
+constexpr int MAX_UNITS_PER_ITEM = 16;   // gemm_row_blocks(false, 8)
 
 // Device weight layout (written by relayout_matrix from packlib "i8"):
 //   matrix [R, K] = R/16 strips of 16 rows; a strip = K/512 superblocks; a superblock (4 groups of 128) =
@@ -92,8 +106,8 @@ struct GemmArgs {
     const uint8_t* base;        // device weight arena
     const uint64_t* off;        // [E+1] byte offset of the matrix of each expert (gate_up or down)
     const int8_t* bits;         // [E+1]
-    const Item* items;
-    const int* n_items;         // device count; blocks with item >= *n_items exit
+    const Item* items;          // work units
+    const int* n_items;         // device count of work units (the persistent grid loops over them)
     const int* slot_token;      // gate_up: B row of slot s is token slot_token[s]; nullptr: row = slot
     const int8_t* xq;           // B rows, int8 [rows, K]
     const float* xs;            // [rows, K/128]
@@ -121,12 +135,14 @@ hipError_t launch_route(const float* part, int nchunks, const float* bias, int T
 // single routing block (T <= block): route + plan + place in one workgroup
 hipError_t launch_route_dispatch(const float* part, int nchunks, const float* bias, int T, int E, int K, int C,
                                  int block, float rscale, int32_t* topk, float* topw, uint32_t* mask, int has_shared,
-                                 int ntok, const int8_t* bits, int32_t* count, int32_t* start, Item* items,
-                                 int* n_items, int32_t* slot_token, float* slot_weight, int32_t* tok_slots,
-                                 hipStream_t st);
+                                 int ntok, const int8_t* bits, int32_t* count, int32_t* start, Item* units_gu,
+                                 Item* units_dn, int* n_units, int32_t* slot_token, float* slot_weight,
+                                 int32_t* tok_slots, hipStream_t st);
 hipError_t launch_masks(const int32_t* topk, int T, int E, int K, int block, uint32_t* mask, hipStream_t st);
+// work units: units_gu / units_dn, n_units[0] / n_units[1]
 hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int has_shared, int ntok,
-                       int32_t* count, int32_t* start, int32_t* bpre, Item* items, int* n_items, hipStream_t st);
+                       const int8_t* bits, int32_t* count, int32_t* start, int32_t* bpre, Item* units_gu,
+                       Item* units_dn, int* n_units, hipStream_t st);
 hipError_t launch_place(const int32_t* topk, const float* topw, const uint32_t* mask, const int32_t* bpre, int T,
                         int E, int K, int block, int has_shared, int32_t* slot_token, float* slot_weight,
                         int32_t* tok_slots, hipStream_t st);

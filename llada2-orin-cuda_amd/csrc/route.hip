@@ -173,47 +173,91 @@ __device__ int block_excl_scan(int v, int* buf, int* total) {
     return incl - v;
 }
 
-// Work-item offsets ordered heaviest first: the shared expert's items, then routed experts by code width
-// (8, 4, 3, 2 bits), expert ascending inside a width -- long workgroups are dispatched first. Wave 0, 4 experts
-// per lane. nit: items per expert (LDS), cls: width class 0..3 per expert (LDS); out: ibase (LDS).
-__device__ void item_offsets_by_width(const int* nit, const int* cls, int E, int shared_items, int* ibase) {
+// Work-unit offsets ordered heaviest first: the shared expert's units, then routed experts by code width (8, 4,
+// 3, 2 bits), expert ascending inside a width -- long workgroups start first. Wave 0, 4 experts per lane.
+// nu_gu / nu_dn: units per expert (LDS); cls: width class 0..3 per expert (LDS); sh_gu / sh_dn: shared units.
+// Out (LDS): base_gu / base_dn per expert, tot[0] / tot[1] = total units. All threads must call it.
+__device__ void unit_offsets(const int* nu_gu, const int* nu_dn, const int* cls, int E, int sh_gu, int sh_dn,
+                             int* base_gu, int* base_dn, int* tot) {
     if (threadIdx.x < 64) {
         const int l = threadIdx.x;
-        int base = shared_items;
+        int bg = sh_gu, bd = sh_dn;
         for (int c = 0; c < 4; ++c) {
-            int v[4], sum = 0;
+            int vg[4], vd[4], sg = 0, sd = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int e = 4 * l + j;
-                v[j] = (e < E && cls[e] == c) ? nit[e] : 0;
-                sum += v[j];
+                const bool in = e < E && cls[e] == c;
+                vg[j] = in ? nu_gu[e] : 0;
+                vd[j] = in ? nu_dn[e] : 0;
+                sg += vg[j];
+                sd += vd[j];
             }
-            int incl = sum;
+            int ig = sg, id = sd;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
-                const int t = __shfl_up(incl, o);
-                if (l >= o) incl += t;
+                const int tg = __shfl_up(ig, o), td = __shfl_up(id, o);
+                if (l >= o) {
+                    ig += tg;
+                    id += td;
+                }
             }
-            int run = base + incl - sum;
+            int rg = bg + ig - sg, rd = bd + id - sd;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int e = 4 * l + j;
-                if (e < E && cls[e] == c) ibase[e] = run;
-                run += v[j];
+                if (e < E && cls[e] == c) {
+                    base_gu[e] = rg;
+                    base_dn[e] = rd;
+                }
+                rg += vg[j];
+                rd += vd[j];
             }
-            base += __shfl(incl, 63);
+            bg += __shfl(ig, 63);
+            bd += __shfl(id, 63);
+        }
+        if (l == 0) {
+            tot[0] = bg;
+            tot[1] = bd;
         }
     }
     __syncthreads();
 }
 
+__device__ __forceinline__ int width_class(int bits) { return bits == 8 ? 0 : bits == 4 ? 1 : bits == 3 ? 2 : 3; }
+
+// the units of expert e: items of <= ntok of its c slots starting at slot st, each split into row blocks
+__device__ void emit_units(int e, int c, int st, int ntok, int bits, int base_gu, int base_dn, Item* units_gu,
+                           Item* units_dn) {
+    const int nit = (c + ntok - 1) / ntok, rg = gemm_row_blocks(false, bits), rd = gemm_row_blocks(true, bits);
+    for (int j = 0; j < nit; ++j) {
+        const int s0 = st + j * ntok, n = min(ntok, c - j * ntok);
+        for (int r = 0; r < rg; ++r) units_gu[base_gu + j * rg + r] = Item{e, s0, n, r};
+        for (int r = 0; r < rd; ++r) units_dn[base_dn + j * rd + r] = Item{e, s0, n, r};
+    }
+}
+
+// the shared expert's units (all T tokens, slots T K + t), the first of both lists; strided over the block
+__device__ void emit_shared_units(int E, int T, int K, int ntok, int bits, Item* units_gu, Item* units_dn) {
+    const int ns = (T + ntok - 1) / ntok, rg = gemm_row_blocks(false, bits), rd = gemm_row_blocks(true, bits);
+    for (int u = threadIdx.x; u < ns * rg; u += blockDim.x) {
+        const int j = u / rg;
+        units_gu[u] = Item{E, T * K + j * ntok, min(ntok, T - j * ntok), u % rg};
+    }
+    for (int u = threadIdx.x; u < ns * rd; u += blockDim.x) {
+        const int j = u / rd;
+        units_dn[u] = Item{E, T * K + j * ntok, min(ntok, T - j * ntok), u % rd};
+    }
+}
+
 struct DispatchOut {         // written by the single-block fused route (decode): the plan + place results
     int has_shared, ntok;
-    const int8_t* bits;      // code width per expert (orders the work items)
+    const int8_t* bits;      // code width per expert [E + 1] (orders and splits the work units)
     int* count;
     int* start;
-    Item* items;
-    int* n_items;
+    Item* units_gu;
+    Item* units_dn;
+    int* n_units;
     int* slot_token;
     float* slot_weight;
     int* tok_slots;
@@ -247,6 +291,7 @@ __global__ void __launch_bounds__(RT_THREADS) route_kernel(const float* __restri
     __shared__ int ibase[MAXE];
     __shared__ int tots[2];
     __shared__ int wcls[MAXE];
+    __shared__ int nu_gu[MAXE], nu_dn[MAXE], ub_gu[MAXE], ub_dn[MAXE], utot[2];
     const int b = blockIdx.x, t0 = b * block, tb = min(block, T - t0), tid = threadIdx.x;
     if (tid < E) {
         sbias[tid] = bias[tid];
@@ -348,29 +393,35 @@ __global__ void __launch_bounds__(RT_THREADS) route_kernel(const float* __restri
     __syncthreads();
     if (tid < E) mask[size_t(b) * E + tid] = tmask[tid];
     if constexpr (FUSED) {
-        // one block: slot ranges = exclusive scan of the per-expert token counts; items of <= ntok slots, the
-        // item list ordered heaviest first (shared expert, then 8 / 4 / 3 / 2-bit experts)
+        // one block: slot ranges = exclusive scan of the per-expert token counts; work units (items of <= ntok
+        // slots, split into row blocks by code width) ordered heaviest first
         const int ns = dout.has_shared ? (T + dout.ntok - 1) / dout.ntok : 0;
+        const int sbits = dout.has_shared ? dout.bits[E] : 8;
         if (tid < E) {
             const int c = __popc(tmask[tid]);
-            cnt[tid] = c;
-            nits[tid] = (c + dout.ntok - 1) / dout.ntok;
             const int b = dout.bits[tid];
-            wcls[tid] = b == 8 ? 0 : b == 4 ? 1 : b == 3 ? 2 : 3;
+            const int nit = (c + dout.ntok - 1) / dout.ntok;
+            cnt[tid] = c;
+            nits[tid] = nit;
+            nu_gu[tid] = nit * gemm_row_blocks(false, b);
+            nu_dn[tid] = nit * gemm_row_blocks(true, b);
+            wcls[tid] = width_class(b);
         }
         __syncthreads();
         expert_scan2(cnt, nits, E, sstart, ibase, tots);
-        item_offsets_by_width(nits, wcls, E, ns, ibase);
-        const int tot_items = tots[1];
+        unit_offsets(nu_gu, nu_dn, wcls, E, ns * gemm_row_blocks(false, sbits), ns * gemm_row_blocks(true, sbits),
+                     ub_gu, ub_dn, utot);
         if (tid < E) {
-            const int c = cnt[tid], st = sstart[tid], ib = ibase[tid], nit = nits[tid];
-            dout.count[tid] = c;
-            dout.start[tid] = st;
-            for (int j = 0; j < nit; ++j)
-                dout.items[ib + j] = Item{tid, st + j * dout.ntok, min(dout.ntok, c - j * dout.ntok), 0};
+            dout.count[tid] = cnt[tid];
+            dout.start[tid] = sstart[tid];
+            emit_units(tid, cnt[tid], sstart[tid], dout.ntok, dout.bits[tid], ub_gu[tid], ub_dn[tid], dout.units_gu,
+                       dout.units_dn);
         }
-        if (tid < ns) dout.items[tid] = Item{E, T * K + tid * dout.ntok, min(dout.ntok, T - tid * dout.ntok), 0};
-        if (tid == 0) *dout.n_items = tot_items + ns;
+        if (ns) emit_shared_units(E, T, K, dout.ntok, sbits, dout.units_gu, dout.units_dn);
+        if (tid == 0) {
+            dout.n_units[0] = utot[0];
+            dout.n_units[1] = utot[1];
+        }
         __syncthreads();
         if (owner) {
             const int t = t0 + tl;
@@ -405,22 +456,33 @@ __global__ void __launch_bounds__(256) masks_kernel(const int* __restrict__ topk
     if (threadIdx.x < E) mask[size_t(b) * E + threadIdx.x] = tmask[threadIdx.x];
 }
 
-// Slot ranges and work items (engine/ops.cu:333-370, :384-410): slots expert-major (expert ascending), inside
-// an expert block-major then token-ascending; items of <= ntok slots per expert; shared-expert items last.
-// One workgroup, thread = expert.
+// Slot ranges and work units (engine/ops.cu:333-370, :384-410): slots expert-major (expert ascending), inside
+// an expert block-major then token-ascending; items of <= ntok slots per expert, split into row blocks by code
+// width, ordered heaviest first (shared expert, then 8 / 4 / 3 / 2-bit experts). One workgroup, thread = expert.
 __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ mask, int T, int E, int K, int block,
-                                                   int has_shared, int ntok, int* __restrict__ count,
-                                                   int* __restrict__ start, int* __restrict__ bpre,
-                                                   Item* __restrict__ items, int* __restrict__ n_items) {
+                                                   int has_shared, int ntok, const int8_t* __restrict__ bits,
+                                                   int* __restrict__ count, int* __restrict__ start,
+                                                   int* __restrict__ bpre, Item* __restrict__ units_gu,
+                                                   Item* __restrict__ units_dn, int* __restrict__ n_units) {
     __shared__ int buf[256];
+    __shared__ int nu_gu[MAXE], nu_dn[MAXE], ub_gu[MAXE], ub_dn[MAXE], wcls[MAXE], utot[2];
     const int e = threadIdx.x, nb = (T + block - 1) / block;
     int c = 0;
     if (e < E)
         for (int b = 0; b < nb; ++b) c += __popc(mask[size_t(b) * E + e]);
-    int tot_slots, tot_items;
+    int tot_slots;
     const int st = block_excl_scan<256>(c, buf, &tot_slots);
-    const int nit = e < E ? (c + ntok - 1) / ntok : 0;
-    const int ib = block_excl_scan<256>(nit, buf, &tot_items);
+    if (e < E) {
+        const int nit = (c + ntok - 1) / ntok, bw = bits[e];
+        nu_gu[e] = nit * gemm_row_blocks(false, bw);
+        nu_dn[e] = nit * gemm_row_blocks(true, bw);
+        wcls[e] = width_class(bw);
+    }
+    __syncthreads();
+    const int ns = has_shared ? (T + ntok - 1) / ntok : 0;
+    const int sbits = has_shared ? bits[E] : 8;
+    unit_offsets(nu_gu, nu_dn, wcls, E, ns * gemm_row_blocks(false, sbits), ns * gemm_row_blocks(true, sbits), ub_gu,
+                 ub_dn, utot);
     if (e < E) {
         count[e] = c;
         start[e] = st;
@@ -429,15 +491,13 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
             bpre[size_t(b) * E + e] = run;
             run += __popc(mask[size_t(b) * E + e]);
         }
-        for (int j = 0; j < nit; ++j) {
-            const int n = min(ntok, c - j * ntok);
-            items[ib + j] = Item{e, st + j * ntok, n, 0};
-        }
+        emit_units(e, c, st, ntok, bits[e], ub_gu[e], ub_dn[e], units_gu, units_dn);
     }
-    const int ns = has_shared ? (T + ntok - 1) / ntok : 0;
-    for (int j = threadIdx.x; j < ns; j += blockDim.x)
-        items[tot_items + j] = Item{E, T * K + j * ntok, min(ntok, T - j * ntok), 0};
-    if (threadIdx.x == 0) *n_items = tot_items + ns;
+    if (ns) emit_shared_units(E, T, K, ntok, sbits, units_gu, units_dn);
+    if (threadIdx.x == 0) {
+        n_units[0] = utot[0];
+        n_units[1] = utot[1];
+    }
 }
 
 // Place every (token, k) pair in its slot; tok_slots[t, K] = the shared slot (or -1). grid nb, 256 threads.
@@ -491,11 +551,12 @@ hipError_t launch_route(const float* part, int nchunks, const float* bias, int T
 
 hipError_t launch_route_dispatch(const float* part, int nchunks, const float* bias, int T, int E, int K, int C,
                                  int block, float rscale, int32_t* topk, float* topw, uint32_t* mask, int has_shared,
-                                 int ntok, const int8_t* bits, int32_t* count, int32_t* start, Item* items,
-                                 int* n_items, int32_t* slot_token, float* slot_weight, int32_t* tok_slots,
-                                 hipStream_t st) {
+                                 int ntok, const int8_t* bits, int32_t* count, int32_t* start, Item* units_gu,
+                                 Item* units_dn, int* n_units, int32_t* slot_token, float* slot_weight,
+                                 int32_t* tok_slots, hipStream_t st) {
     if (T > block) return hipErrorInvalidValue;
-    const DispatchOut d{has_shared, ntok, bits, count, start, items, n_items, slot_token, slot_weight, tok_slots};
+    const DispatchOut d{has_shared, ntok, bits, count, start, units_gu, units_dn, n_units, slot_token, slot_weight,
+                        tok_slots};
     route_kernel<true><<<1, RT_THREADS, 0, st>>>(part, nchunks, bias, T, E, K, C, block, rscale, topk, topw, mask, d);
     return hipGetLastError();
 }
@@ -507,8 +568,10 @@ hipError_t launch_masks(const int32_t* topk, int T, int E, int K, int block, uin
 }
 
 hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int has_shared, int ntok,
-                       int32_t* count, int32_t* start, int32_t* bpre, Item* items, int* n_items, hipStream_t st) {
-    plan_kernel<<<1, 256, 0, st>>>(mask, T, E, K, block, has_shared, ntok, count, start, bpre, items, n_items);
+                       const int8_t* bits, int32_t* count, int32_t* start, int32_t* bpre, Item* units_gu,
+                       Item* units_dn, int* n_units, hipStream_t st) {
+    plan_kernel<<<1, 256, 0, st>>>(mask, T, E, K, block, has_shared, ntok, bits, count, start, bpre, units_gu,
+                                   units_dn, n_units);
     return hipGetLastError();
 }
 
