@@ -20,6 +20,10 @@ _HERE = Path(__file__).resolve().parent
 LIB_PATH = _HERE / "libllmoe.so"
 
 LLMOE_OK = 0
+LLMOE_EINVAL = -1   # bad argument or shape
+LLMOE_ENOMEM = -2
+LLMOE_EHIP = -3
+LLMOE_ESTATE = -4
 
 
 class LLMoEError(RuntimeError):

@@ -1,0 +1,75 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function include/llmoe.h declares, and
+rejects bad layer descriptions before touching the device."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import llmoe
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared():
+    text = (ROOT / "include" / "llmoe.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b(llmoe_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not llmoe.LIB_PATH.exists():
+        pytest.skip("libllmoe.so not built (python -c 'import __graft_entry__ as g; g.build()')")
+    return llmoe.load_library()
+
+
+def test_header_and_binding_agree():
+    assert declared() == sorted(llmoe.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared():
+        assert hasattr(lib, name), name
+
+
+def _create(desc_kw, bits=None, blob_bytes=None):
+    d = llmoe.LayerDesc(hidden=2048, inter=512, n_experts=64, top_k=8, pool=48, block=32, routed_scale=2.5,
+                        has_shared=0, max_tokens=32)
+    for k, v in desc_kw.items():
+        setattr(d, k, v)
+    E = d.n_experts + d.has_shared
+    bits = np.full(max(E, 1), 2, np.int8) if bits is None else bits
+    eb = llmoe.synth.expert_bytes(2)
+    gu = np.arange(max(E, 1), dtype=np.uint64) * np.uint64(eb)
+    dd = gu + np.uint64(llmoe.synth.matrix_bytes(1024, 2048, 2))
+    blob = np.zeros(16, np.uint8)
+    nbytes = eb * E if blob_bytes is None else blob_bytes
+    bias = np.zeros(max(E, 1), np.float32)
+    out = ctypes.c_void_p()
+    rc = llmoe.load_library().llmoe_layer_create(ctypes.byref(d), blob.ctypes.data, ctypes.c_size_t(nbytes),
+                                                 gu.ctypes.data, dd.ctypes.data, bits.ctypes.data, None,
+                                                 bias.ctypes.data, ctypes.byref(out))
+    return rc, llmoe.load_library().llmoe_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(hidden=1024), "hidden"), (dict(inter=256), "inter"), (dict(n_experts=100), "n_experts"),
+    (dict(top_k=9), "top_k"), (dict(pool=4), "pool"), (dict(block=64), "block"), (dict(max_tokens=0), "max_tokens"),
+])
+def test_create_rejects_bad_desc(lib, kw, msg):
+    rc, err = _create(kw)
+    assert rc == llmoe.LLMOE_EINVAL and msg in err
+
+
+def test_create_rejects_bad_bits_and_short_blob(lib):
+    bits = np.full(64, 2, np.int8)
+    bits[7] = 5
+    rc, err = _create({}, bits=bits)
+    assert rc == llmoe.LLMOE_EINVAL and "expert 7" in err
+    rc, err = _create({}, blob_bytes=1000)
+    assert rc == llmoe.LLMOE_EINVAL and "beyond the blob" in err
