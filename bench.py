@@ -166,6 +166,31 @@ def stack_config(llmoe, synth, torch, steps, warmup, nlayers=20, T=2048):
     return res
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "expert_gemm_gate_up_config1_traffic.txt"
+
+
+def measured_traffic():
+    """HBM bytes per gate_up launch from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE per
+    dispatch, calibrated against a copy kernel of known size); None when no such summary exists."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch"):
+            return float(line.split("=")[1].split()[0])
+    return None
+
+
+def copy_calibration(torch, mib=512, reps=3):
+    """Plain device copies of a known size, so counter runs can calibrate FETCH_SIZE / WRITE_SIZE per byte."""
+    a = torch.empty(mib << 20, dtype=torch.uint8, device="cuda:0")
+    b = torch.empty_like(a)
+    a.fill_(1)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"[bench] copy calibration: {reps} copies of {mib} MiB")
+
+
 def cpu_baseline(L, x_np, pool, seconds):
     import oracle
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
@@ -192,6 +217,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-headline", action="store_true", help="config 1 only (profiling runs)")
+    ap.add_argument("--copy-calibration", action="store_true", help="run 512 MiB device copies first (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (expert sharding is described in "
@@ -204,6 +230,8 @@ def main():
     from llmoe import synth
     llmoe.load_library()
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        copy_calibration(torch)
 
     log("[bench] config 1 (headline)")
     c1, (L1, G1s, x1, _, _) = one_layer_config(llmoe, synth, torch, "config 1: 32 tokens, mixed 2/3/4-bit + W8A8 "
@@ -225,8 +253,8 @@ def main():
     gu_s = p["gate_up"] * 1e-3
     achieved = c1["gate_up_bytes"] / gu_s / 1e9
     roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": achieved / PEAK_HBM_GBS, "traffic": None,
-                "kernel": "stream_gemm<gate_up> (config 1)", "bytes_per_launch": c1["gate_up_bytes"],
+                "frac": achieved / PEAK_HBM_GBS, "traffic": measured_traffic(),
+                "kernel": "expert_gemm<gate_up> (config 1)", "bytes_per_launch": c1["gate_up_bytes"],
                 "avg_launch_ms": p["gate_up"]}
     cpu = None
     if not args.no_cpu:

@@ -47,7 +47,7 @@ typedef struct llmoe_layer llmoe_layer;
 typedef void* llmoe_stream; /* hipStream_t */
 
 typedef struct {
-    int hidden;          /* H, multiple of 512 (2048 in LLaDA2.2-mini) */
+    int hidden;          /* H, must be 2048 (LLaDA2.2-mini; the GEMM geometry is compiled for it) */
     int inter;           /* I, must be 512 (FWHT-512 on the down input) */
     int n_experts;       /* E routed experts, <= 256 */
     int top_k;           /* K experts per token, <= 8 */
