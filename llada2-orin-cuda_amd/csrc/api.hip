@@ -64,23 +64,27 @@ struct llmoe_layer {
     int32_t* topk = nullptr; float* topw = nullptr;
     uint32_t* mask = nullptr; int32_t* bpre = nullptr;
     int32_t* count = nullptr; int32_t* start = nullptr;
-    Item* units_gu = nullptr; Item* units_dn = nullptr; int* n_units = nullptr;   // GEMM work units
+    Item* units_gu = nullptr; Item* units_dn = nullptr; int* n_units = nullptr;   // streamed GEMM work units
+    Item* tunits_gu = nullptr; Item* tunits_dn = nullptr;                          // tiled GEMM work units
     int32_t* slot_token = nullptr; float* slot_weight = nullptr; int32_t* tok_slots = nullptr;
     uint16_t* Z = nullptr; int8_t* zq = nullptr; float* zs = nullptr; int32_t* zsum = nullptr;
     float* Y = nullptr;
     Item* p_item = nullptr; int* p_count = nullptr;  // unit list of llmoe_group_products
     Item p_item_host[MAX_UNITS_PER_ITEM] = {}; int p_count_host = 1;
     size_t items_cap = 0;                           // work items (before the split into row blocks)
+    size_t chunks_cap = 0;                          // tiled chunks (before the split into row blocks)
     // routing state
     int routed_T = -1, ntok = 16, max_items = 0;
+    bool tiled = false;                             // the routing of routed_T may have tiled units
     // stage timing
     bool profiling = false;
     hipEvent_t ev[2 * LLMOE_N_STAGES] = {};
     bool ran[LLMOE_N_STAGES] = {};
     // the latest llmoe_experts launch (for llmoe_layer_time_stage)
-    GemmArgs last_gu{}, last_dn{};
+    GemmArgs last_gu{}, last_dn{}, last_tgu{}, last_tdn{};
     float* last_out = nullptr;
     int last_S = 0, last_T = 0, last_nt = 1;
+    bool last_tiled = false;
     bool have_last = false;
     std::vector<void*> allocs;
 
@@ -115,16 +119,16 @@ int check_layer(const llmoe_layer* L) {
 
 int nblocks(const llmoe_layer* L, int T) { return (T + L->d.block - 1) / L->d.block; }
 
-// tokens per work item and the item capacity for T tokens
+// streamed work items hold 16 slots; the item capacity for T tokens (experts with more than TILED_MIN slots take
+// tiled units instead when T > TILED_MIN)
 void choose_items(llmoe_layer* L, int T) {
     const auto& d = L->d;
     const long eff = std::min<long>(d.n_experts, long(nblocks(L, T)) * std::min(d.pool, d.n_experts));
-    const long avg = (long(T) * d.top_k + eff - 1) / eff;
-    const int nt = avg <= 8 ? 1 : avg <= 24 ? 2 : 4;
-    L->ntok = 16 * nt;
+    L->ntok = 16;
     const long routed = eff + (long(T) * d.top_k + L->ntok - 1) / L->ntok;
     const long shared = d.has_shared ? (T + L->ntok - 1) / L->ntok : 0;
     L->max_items = int(routed + shared);
+    L->tiled = T > TILED_MIN;
 }
 
 int check_T(const llmoe_layer* L, int T) {
@@ -132,9 +136,11 @@ int check_T(const llmoe_layer* L, int T) {
     return LLMOE_OK;
 }
 
-// expert GEMM of one stage (items of 16 * nt slots)
-hipError_t launch_gemm(int mode, int nt, const GemmArgs& g, int max_items, hipStream_t st) {
-    return launch_expert_gemm(mode, nt, g, max_items, st);
+// expert GEMMs of one stage: the streamed units, then (if the routing may have any) the tiled units
+hipError_t launch_gemm(int mode, const GemmArgs& g, const GemmArgs& tg, bool tiled, hipStream_t st) {
+    hipError_t e = launch_expert_gemm(mode, 1, g, 0, st);
+    if (e == hipSuccess && tiled) e = launch_tiled_gemm(mode, tg, st);
+    return e;
 }
 
 int plan_and_place(llmoe_layer* L, const int32_t* topk, const float* topw, int T, hipStream_t st) {
@@ -142,8 +148,9 @@ int plan_and_place(llmoe_layer* L, const int32_t* topk, const float* topw, int T
     choose_items(L, T);
     if (size_t(L->max_items) > L->items_cap) return fail(LLMOE_EINVAL, "item capacity exceeded");
     L->mark(LLMOE_STAGE_DISPATCH, false, st);
-    HIPCHECK(launch_plan(L->mask, T, d.n_experts, d.top_k, d.block, d.has_shared, L->ntok, L->bits_d, L->count,
-                         L->start, L->bpre, L->units_gu, L->units_dn, L->n_units, st));
+    HIPCHECK(launch_plan(L->mask, T, d.n_experts, d.top_k, d.block, d.has_shared, L->ntok, L->tiled ? 1 : 0,
+                         L->bits_d, L->count, L->start, L->bpre, L->units_gu, L->units_dn, L->tunits_gu,
+                         L->tunits_dn, L->n_units, st));
     HIPCHECK(launch_place(topk, topw, L->mask, L->bpre, T, d.n_experts, d.top_k, d.block, d.has_shared,
                           L->slot_token, L->slot_weight, L->tok_slots, st));
     L->mark(LLMOE_STAGE_DISPATCH, true, st);
@@ -186,6 +193,7 @@ int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t bl
     }
     if (!g_setup_done) {
         g_setup = gemm_setup();
+        if (g_setup == hipSuccess) g_setup = tiled_setup();
         g_setup_done = true;
     }
     if (g_setup != hipSuccess) return fail(LLMOE_EHIP, "gemm_setup: %s", hipGetErrorString(g_setup));
@@ -262,7 +270,10 @@ int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t bl
     L->items_cap = E + (Tm * K + 15) / 16 + (Tm + 15) / 16 + 2;
     ALLOC(L->units_gu, L->items_cap * MAX_UNITS_PER_ITEM);
     ALLOC(L->units_dn, L->items_cap * MAX_UNITS_PER_ITEM);
-    ALLOC(L->n_units, 2);
+    ALLOC(L->n_units, 4);
+    L->chunks_cap = E + (Tm * K + TILED_NTOK - 1) / TILED_NTOK + (Tm + TILED_NTOK - 1) / TILED_NTOK + 2;
+    ALLOC(L->tunits_gu, L->chunks_cap * MAX_TILED_UNITS_PER_CHUNK);
+    ALLOC(L->tunits_dn, L->chunks_cap * MAX_TILED_UNITS_PER_CHUNK);
     ALLOC(L->slot_token, S);
     ALLOC(L->slot_weight, S);
     ALLOC(L->tok_slots, Tm * (K + 1));
@@ -351,7 +362,6 @@ int llmoe_experts(llmoe_layer* L, const int8_t* xq, const float* xs, const int32
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const int H = d.hidden, I = d.inter, K = d.top_k;
     const int S = T * K + (d.has_shared ? T : 0);
-    const int nt = L->ntok / 16;
     GemmArgs g{};
     g.base = L->arena;
     g.bits = L->bits_d;
@@ -363,9 +373,13 @@ int llmoe_experts(llmoe_layer* L, const int8_t* xq, const float* xs, const int32
     g.slot_token = L->slot_token;
     g.xq = xq; g.xs = xs; g.xsum = xsum;
     g.K = H; g.R = 2 * I; g.Z = L->Z;
+    GemmArgs tg = g;
+    tg.items = L->tunits_gu;
+    tg.n_items = L->n_units + 2;
     L->last_gu = g;
+    L->last_tgu = tg;
     L->mark(LLMOE_STAGE_GATE_UP, false, st);
-    HIPCHECK(launch_gemm(GEMM_GATE_UP, nt, g, L->max_items, st));
+    HIPCHECK(launch_gemm(GEMM_GATE_UP, g, tg, L->tiled, st));
     L->mark(LLMOE_STAGE_GATE_UP, true, st);
     L->mark(LLMOE_STAGE_FWHT, false, st);
     HIPCHECK(launch_fwht_a8(L->Z, S, L->zq, L->zs, L->zsum, st));
@@ -377,10 +391,14 @@ int llmoe_experts(llmoe_layer* L, const int8_t* xq, const float* xs, const int32
     g.slot_token = nullptr;
     g.xq = L->zq; g.xs = L->zs; g.xsum = L->zsum;
     g.K = I; g.R = H; g.Z = nullptr; g.Y = L->Y;
+    tg = g;
+    tg.items = L->tunits_dn;
+    tg.n_items = L->n_units + 3;
     L->last_dn = g;
-    L->last_S = S; L->last_T = T; L->last_nt = nt; L->last_out = out; L->have_last = true;
+    L->last_tdn = tg;
+    L->last_S = S; L->last_T = T; L->last_tiled = L->tiled; L->last_out = out; L->have_last = true;
     L->mark(LLMOE_STAGE_DOWN, false, st);
-    HIPCHECK(launch_gemm(GEMM_DOWN, nt, g, L->max_items, st));
+    HIPCHECK(launch_gemm(GEMM_DOWN, g, tg, L->tiled, st));
     L->mark(LLMOE_STAGE_DOWN, true, st);
     L->mark(LLMOE_STAGE_COMBINE, false, st);
     HIPCHECK(launch_combine(L->Y, L->tok_slots, T, H, K + (d.has_shared ? 1 : 0), K + 1, out, st));
@@ -426,8 +444,8 @@ namespace {
 hipError_t relaunch_stage(llmoe_layer* L, int stage, hipStream_t st) {
     const auto& d = L->d;
     switch (stage) {
-        case LLMOE_STAGE_GATE_UP: return launch_gemm(GEMM_GATE_UP, L->last_nt, L->last_gu, L->max_items, st);
-        case LLMOE_STAGE_DOWN: return launch_gemm(GEMM_DOWN, L->last_nt, L->last_dn, L->max_items, st);
+        case LLMOE_STAGE_GATE_UP: return launch_gemm(GEMM_GATE_UP, L->last_gu, L->last_tgu, L->last_tiled, st);
+        case LLMOE_STAGE_DOWN: return launch_gemm(GEMM_DOWN, L->last_dn, L->last_tdn, L->last_tiled, st);
         case LLMOE_STAGE_FWHT: return launch_fwht_a8(L->Z, L->last_S, L->zq, L->zs, L->zsum, st);
         case LLMOE_STAGE_COMBINE:
             return launch_combine(L->Y, L->tok_slots, L->last_T, d.hidden, d.top_k + (d.has_shared ? 1 : 0),

@@ -2,7 +2,7 @@
 //
 // Math (engine/moe_i8.cu:1-14, :364-383): per 128-group g of the reduction
 //     P_g[r, n] = sum_{k in g} code[r, k] xq[n, k] - zero[r, g] Sxq[n, g]          (exact int32)
-//     acc[r, n] = fma(scale_w[r, g] * scale_x[n, g], float(P_g[r, n]), acc[r, n])  (fp32, g ascending)
+//     acc[r, n] = fma(scale_w[r, g] * scale_x[n, g], float(P_g[r, n]), acc[r, n])  (fp32, g ascending from 0)
 // The zero-point term enters as the MFMA's initial accumulator, so no integer work follows the MFMA.
 // 8-bit codes are stored as code - 128 (signed), and their zero as zero - 128 in the same product.
 //
@@ -219,11 +219,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
         const int n = nt * 16 + col;
         wts[nt] = (MODE == GEMM_DOWN && n < ntok) ? a.slot_weight[it.slot0 + n] : 0.0f;
     }
-    float acc[NT][4], tot[NT][4];
+    float acc[NT][4];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[nt][v] = tot[nt][v] = 0.0f;
+        for (int v = 0; v < 4; ++v) acc[nt][v] = 0.0f;
 
     // the wave's SPW strips are NSTEP consecutive superblocks in memory, streamed as one ring (slot of step u =
     // u % D). The steps are unrolled at compile time: across a loop back-edge the compiler would wait for every
@@ -286,35 +286,25 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (!Geo<MODE>::PRODUCTS) {
-            // superblock partial (an fma chain over its 4 groups) added to the row total in superblock order
+        if constexpr (!Geo<MODE>::PRODUCTS && sb == NSB - 1) {   // strip done: fused epilogue
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    tot[nt][v] = tot[nt][v] + acc[nt][v];
-                    acc[nt][v] = 0.0f;
-                }
-            if constexpr (sb == NSB - 1) {
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    const int n = nt * 16 + col;
-                    if (n < ntok) {
-                        const int slot = it.slot0 + n;
-                        if constexpr (MODE == GEMM_GATE_UP) {
-                            // lane quad q holds rows gate 8 strip + 2q, up (same), gate + 1, up + 1
-                            const uint32_t z0 = f32_to_f16_bits(silu_f32(tot[nt][0]) * tot[nt][1]);
-                            const uint32_t z1 = f32_to_f16_bits(silu_f32(tot[nt][2]) * tot[nt][3]);
-                            *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
-                        } else {
-                            const float w = wts[nt];
-                            *reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q) =
-                                make_float4(w * tot[nt][0], w * tot[nt][1], w * tot[nt][2], w * tot[nt][3]);
-                        }
+            for (int nt = 0; nt < NT; ++nt) {
+                const int n = nt * 16 + col;
+                if (n < ntok) {
+                    const int slot = it.slot0 + n;
+                    if constexpr (MODE == GEMM_GATE_UP) {
+                        // lane quad q holds rows gate 8 strip + 2q, up (same), gate + 1, up + 1
+                        const uint32_t z0 = f32_to_f16_bits(silu_f32(acc[nt][0]) * acc[nt][1]);
+                        const uint32_t z1 = f32_to_f16_bits(silu_f32(acc[nt][2]) * acc[nt][3]);
+                        *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
+                    } else {
+                        const float w = wts[nt];
+                        *reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q) =
+                            make_float4(w * acc[nt][0], w * acc[nt][1], w * acc[nt][2], w * acc[nt][3]);
                     }
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) tot[nt][v] = 0.0f;
                 }
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[nt][v] = 0.0f;
             }
         }
         // refill the slot just consumed with step u + D
@@ -370,28 +360,17 @@ hipError_t launch_t(const GemmArgs& a, int, hipStream_t st) {
 hipError_t gemm_setup() {
     hipError_t e;
     if ((e = set_attr<GEMM_GATE_UP, 1>()) != hipSuccess) return e;
-    if ((e = set_attr<GEMM_GATE_UP, 2>()) != hipSuccess) return e;
-    if ((e = set_attr<GEMM_GATE_UP, 4>()) != hipSuccess) return e;
     if ((e = set_attr<GEMM_DOWN, 1>()) != hipSuccess) return e;
-    if ((e = set_attr<GEMM_DOWN, 2>()) != hipSuccess) return e;
-    if ((e = set_attr<GEMM_DOWN, 4>()) != hipSuccess) return e;
     if ((e = set_attr<GEMM_PRODUCTS_GATE_UP, 4>()) != hipSuccess) return e;
     if ((e = set_attr<GEMM_PRODUCTS_DOWN, 4>()) != hipSuccess) return e;
     return hipSuccess;
 }
 
-// mode: GemmMode; nt: 1, 2 or 4 (16-token tiles per item; the products modes always run NT = 4).
+// mode: GemmMode; nt: 16-token tiles per work item, 1 for the layer GEMMs (experts with many tokens take the
+// tiled kernel), 4 for the products modes.
 hipError_t launch_expert_gemm(int mode, int nt, const GemmArgs& a, int max_items, hipStream_t st) {
-    if (mode == GEMM_GATE_UP) {
-        if (nt == 1) return launch_t<GEMM_GATE_UP, 1>(a, max_items, st);
-        if (nt == 2) return launch_t<GEMM_GATE_UP, 2>(a, max_items, st);
-        return launch_t<GEMM_GATE_UP, 4>(a, max_items, st);
-    }
-    if (mode == GEMM_DOWN) {
-        if (nt == 1) return launch_t<GEMM_DOWN, 1>(a, max_items, st);
-        if (nt == 2) return launch_t<GEMM_DOWN, 2>(a, max_items, st);
-        return launch_t<GEMM_DOWN, 4>(a, max_items, st);
-    }
+    if (mode == GEMM_GATE_UP) return nt == 1 ? launch_t<GEMM_GATE_UP, 1>(a, max_items, st) : hipErrorInvalidValue;
+    if (mode == GEMM_DOWN) return nt == 1 ? launch_t<GEMM_DOWN, 1>(a, max_items, st) : hipErrorInvalidValue;
     if (mode == GEMM_PRODUCTS_GATE_UP) return launch_t<GEMM_PRODUCTS_GATE_UP, 4>(a, max_items, st);
     return launch_t<GEMM_PRODUCTS_DOWN, 4>(a, max_items, st);
 }

@@ -34,6 +34,25 @@ __host__ __device__ constexpr int gemm_row_blocks(bool down, int bits) {
 }
 constexpr int MAX_UNITS_PER_ITEM = 16;   // gemm_row_blocks(false, 8)
 
+// Tiled GEMM (experts with many tokens): a work unit is a chunk of <= TILED_NTOK slots of one expert and a
+// range of row blocks (Item.rb = first | count << 16); the workgroup stages the chunk's activations in LDS once
+// and its TILED_WAVES waves stream tiled_spw strips each per row block. An expert takes tiled units when it has
+// more than TILED_MIN slots, otherwise streamed units of 16 slots.
+constexpr int TILED_NTOK = 64;
+constexpr int TILED_MIN = 40;
+constexpr int TILED_WAVES = 8;
+__host__ __device__ constexpr int tiled_spw(int bits) { return bits == 8 ? 1 : 2; }
+__host__ __device__ constexpr int tiled_row_blocks(bool down, int bits) {
+    return (down ? 2048 : 1024) / (16 * TILED_WAVES * tiled_spw(bits));
+}
+// chunks of an expert with c slots: n = ceil(c / TILED_NTOK) chunks of `per` slots (a multiple of 16), the last
+// one shorter
+__host__ __device__ constexpr int tiled_chunks(int c) { return (c + TILED_NTOK - 1) / TILED_NTOK; }
+__host__ __device__ constexpr int tiled_per(int c) {
+    return c <= 0 ? 0 : (((c + tiled_chunks(c) - 1) / tiled_chunks(c)) + 15) / 16 * 16;
+}
+constexpr int MAX_TILED_UNITS_PER_CHUNK = 4;    // row-block ranges per chunk (tiled_split)
+
 // Device weight layout (written by relayout_matrix from packlib "i8"):
 //   matrix [R, K] = R/16 strips of 16 rows; a strip = K/512 superblocks; a superblock (4 groups of 128) =
 //     BITS x 1024 B of codes: load i of lane l (64 lanes) at i*1024 + 16 l (one dwordx4 per lane and load)
@@ -124,6 +143,9 @@ enum GemmMode { GEMM_GATE_UP = 0, GEMM_DOWN = 1, GEMM_PRODUCTS_GATE_UP = 2, GEMM
 
 hipError_t gemm_setup();   // function attributes (dynamic LDS), once per process
 hipError_t launch_expert_gemm(int mode, int nt, const GemmArgs& a, int max_items, hipStream_t st);
+// tiled units (a.items / a.n_items): mode GEMM_GATE_UP or GEMM_DOWN
+hipError_t tiled_setup();
+hipError_t launch_tiled_gemm(int mode, const GemmArgs& a, hipStream_t st);
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, int R, int K, int bits, int gate_up, hipStream_t st);
 hipError_t launch_quant_a8(const float* x, int rows, int cols, int8_t* q, float* s, int* sum, hipStream_t st);
 hipError_t launch_fwht_a8(const uint16_t* Z, int nslots, int8_t* q, float* s, int* sum, hipStream_t st);
@@ -139,10 +161,11 @@ hipError_t launch_route_dispatch(const float* part, int nchunks, const float* bi
                                  Item* units_dn, int* n_units, int32_t* slot_token, float* slot_weight,
                                  int32_t* tok_slots, hipStream_t st);
 hipError_t launch_masks(const int32_t* topk, int T, int E, int K, int block, uint32_t* mask, hipStream_t st);
-// work units: units_gu / units_dn, n_units[0] / n_units[1]
-hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int has_shared, int ntok,
+// work units: streamed units_gu / units_dn (n_units[0] / [1], items of <= ntok slots), tiled tunits_gu /
+// tunits_dn (n_units[2] / [3]) for experts with more than TILED_MIN slots when `tiled` is set
+hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int has_shared, int ntok, int tiled,
                        const int8_t* bits, int32_t* count, int32_t* start, int32_t* bpre, Item* units_gu,
-                       Item* units_dn, int* n_units, hipStream_t st);
+                       Item* units_dn, Item* tunits_gu, Item* tunits_dn, int* n_units, hipStream_t st);
 hipError_t launch_place(const int32_t* topk, const float* topw, const uint32_t* mask, const int32_t* bpre, int T,
                         int E, int K, int block, int has_shared, int32_t* slot_token, float* slot_weight,
                         int32_t* tok_slots, hipStream_t st);

@@ -250,6 +250,34 @@ __device__ void emit_shared_units(int E, int T, int K, int ntok, int bits, Item*
     }
 }
 
+// tiled units of expert e (c slots from slot st): chunks of tiled_per(c) slots, each split into `split` ranges
+// of row blocks (Item.rb = first | count << 16)
+__device__ __forceinline__ int rb_range(int R, int split, int r) { return (r * (R / split)) | ((R / split) << 16); }
+__device__ void emit_tiled_units(int e, int c, int st, int bits, int split, int base_gu, int base_dn, Item* tunits_gu,
+                                 Item* tunits_dn) {
+    const int nch = tiled_chunks(c), per = tiled_per(c);
+    const int rg = tiled_row_blocks(false, bits), rd = tiled_row_blocks(true, bits);
+    for (int j = 0; j < nch; ++j) {
+        const int s0 = st + j * per, n = min(per, c - j * per);
+        for (int r = 0; r < split; ++r) {
+            tunits_gu[base_gu + j * split + r] = Item{e, s0, n, rb_range(rg, split, r)};
+            tunits_dn[base_dn + j * split + r] = Item{e, s0, n, rb_range(rd, split, r)};
+        }
+    }
+}
+
+// the shared expert's tiled units (all T tokens, slots T K + t), the first of both tiled lists
+__device__ void emit_shared_tiled_units(int E, int T, int K, int bits, int split, Item* tunits_gu, Item* tunits_dn) {
+    const int nch = tiled_chunks(T), per = tiled_per(T);
+    const int rg = tiled_row_blocks(false, bits), rd = tiled_row_blocks(true, bits);
+    for (int u = threadIdx.x; u < nch * split; u += blockDim.x) {
+        const int j = u / split, r = u % split;
+        const Item it{E, T * K + j * per, min(per, T - j * per), 0};
+        tunits_gu[u] = Item{it.expert, it.slot0, it.ntok, rb_range(rg, split, r)};
+        tunits_dn[u] = Item{it.expert, it.slot0, it.ntok, rb_range(rd, split, r)};
+    }
+}
+
 struct DispatchOut {         // written by the single-block fused route (decode): the plan + place results
     int has_shared, ntok;
     const int8_t* bits;      // code width per expert [E + 1] (orders and splits the work units)
@@ -457,32 +485,49 @@ __global__ void __launch_bounds__(256) masks_kernel(const int* __restrict__ topk
 }
 
 // Slot ranges and work units (engine/ops.cu:333-370, :384-410): slots expert-major (expert ascending), inside
-// an expert block-major then token-ascending; items of <= ntok slots per expert, split into row blocks by code
-// width, ordered heaviest first (shared expert, then 8 / 4 / 3 / 2-bit experts). One workgroup, thread = expert.
+// an expert block-major then token-ascending. An expert with more than TILED_MIN slots (when `tiled`) gets tiled
+// units (chunks of <= TILED_NTOK slots x tiled row blocks), otherwise streamed units (items of <= ntok slots x
+// streamed row blocks). Both lists are ordered heaviest first (shared expert, then 8 / 4 / 3 / 2-bit experts).
+// One workgroup, thread = expert.
 __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ mask, int T, int E, int K, int block,
-                                                   int has_shared, int ntok, const int8_t* __restrict__ bits,
-                                                   int* __restrict__ count, int* __restrict__ start,
-                                                   int* __restrict__ bpre, Item* __restrict__ units_gu,
-                                                   Item* __restrict__ units_dn, int* __restrict__ n_units) {
+                                                   int has_shared, int ntok, int tiled,
+                                                   const int8_t* __restrict__ bits, int* __restrict__ count,
+                                                   int* __restrict__ start, int* __restrict__ bpre,
+                                                   Item* __restrict__ units_gu, Item* __restrict__ units_dn,
+                                                   Item* __restrict__ tunits_gu, Item* __restrict__ tunits_dn,
+                                                   int* __restrict__ n_units) {
     __shared__ int buf[256];
     __shared__ int nu_gu[MAXE], nu_dn[MAXE], ub_gu[MAXE], ub_dn[MAXE], wcls[MAXE], utot[2];
+    __shared__ int tu_gu[MAXE], tu_dn[MAXE], tb_gu[MAXE], tb_dn[MAXE], ttot[2];
     const int e = threadIdx.x, nb = (T + block - 1) / block;
     int c = 0;
     if (e < E)
         for (int b = 0; b < nb; ++b) c += __popc(mask[size_t(b) * E + e]);
     int tot_slots;
     const int st = block_excl_scan<256>(c, buf, &tot_slots);
+    const bool big = tiled && c > TILED_MIN;
+    const bool sbig = has_shared && tiled && T > TILED_MIN;
+    const int nsch = sbig ? tiled_chunks(T) : 0;
+    // row-block ranges per chunk: enough tiled units to fill the GPU (split a chunk's rows when chunks are few)
+    int all_chunks;
+    block_excl_scan<256>(e < E && big ? tiled_chunks(c) : 0, buf, &all_chunks);
+    all_chunks += nsch;
+    const int split = all_chunks >= 384 ? 1 : all_chunks >= 192 ? 2 : 4;
     if (e < E) {
-        const int nit = (c + ntok - 1) / ntok, bw = bits[e];
+        const int bw = bits[e];
+        const int nit = big ? 0 : (c + ntok - 1) / ntok, nch = big ? tiled_chunks(c) : 0;
         nu_gu[e] = nit * gemm_row_blocks(false, bw);
         nu_dn[e] = nit * gemm_row_blocks(true, bw);
+        tu_gu[e] = nch * split;
+        tu_dn[e] = nch * split;
         wcls[e] = width_class(bw);
     }
     __syncthreads();
-    const int ns = has_shared ? (T + ntok - 1) / ntok : 0;
     const int sbits = has_shared ? bits[E] : 8;
+    const int ns = has_shared && !sbig ? (T + ntok - 1) / ntok : 0;
     unit_offsets(nu_gu, nu_dn, wcls, E, ns * gemm_row_blocks(false, sbits), ns * gemm_row_blocks(true, sbits), ub_gu,
                  ub_dn, utot);
+    unit_offsets(tu_gu, tu_dn, wcls, E, nsch * split, nsch * split, tb_gu, tb_dn, ttot);
     if (e < E) {
         count[e] = c;
         start[e] = st;
@@ -491,12 +536,16 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
             bpre[size_t(b) * E + e] = run;
             run += __popc(mask[size_t(b) * E + e]);
         }
-        emit_units(e, c, st, ntok, bits[e], ub_gu[e], ub_dn[e], units_gu, units_dn);
+        if (big) emit_tiled_units(e, c, st, bits[e], split, tb_gu[e], tb_dn[e], tunits_gu, tunits_dn);
+        else emit_units(e, c, st, ntok, bits[e], ub_gu[e], ub_dn[e], units_gu, units_dn);
     }
     if (ns) emit_shared_units(E, T, K, ntok, sbits, units_gu, units_dn);
+    if (sbig) emit_shared_tiled_units(E, T, K, sbits, split, tunits_gu, tunits_dn);
     if (threadIdx.x == 0) {
         n_units[0] = utot[0];
         n_units[1] = utot[1];
+        n_units[2] = ttot[0];
+        n_units[3] = ttot[1];
     }
 }
 
@@ -567,11 +616,11 @@ hipError_t launch_masks(const int32_t* topk, int T, int E, int K, int block, uin
     return hipGetLastError();
 }
 
-hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int has_shared, int ntok,
+hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int has_shared, int ntok, int tiled,
                        const int8_t* bits, int32_t* count, int32_t* start, int32_t* bpre, Item* units_gu,
-                       Item* units_dn, int* n_units, hipStream_t st) {
-    plan_kernel<<<1, 256, 0, st>>>(mask, T, E, K, block, has_shared, ntok, bits, count, start, bpre, units_gu,
-                                   units_dn, n_units);
+                       Item* units_dn, Item* tunits_gu, Item* tunits_dn, int* n_units, hipStream_t st) {
+    plan_kernel<<<1, 256, 0, st>>>(mask, T, E, K, block, has_shared, ntok, tiled, bits, count, start, bpre, units_gu,
+                                   units_dn, tunits_gu, tunits_dn, n_units);
     return hipGetLastError();
 }
 

@@ -1,0 +1,436 @@
+// Tiled routed-expert W(2/3/4/8)·A8 GEMMs for experts with many tokens (prefill / batched denoising), gfx950
+// int8 MFMA. Same math and the same fp32 operation sequence as expert_gemm.hip (engine/moe_i8.cu:1-14,
+// :364-383): per 128-group g, P_g = sum code xq - zero Sxq exact in int32, then
+// acc = fma(scale_w scale_x, float(P_g), acc) for g ascending from 0.
+//
+// Work unit: <= TILED_NTOK (64) slots of one expert and a range of row blocks. The workgroup (8 waves) first
+// copies the chunk's int8 activation rows for the WHOLE reduction (64 x K bytes, XOR-swizzled 16-byte chunks so
+// the MFMA operand reads are conflict-free), their scales and sums into LDS, then every wave streams its own
+// tiled_spw(bits) 16-row strips of each row block through registers: each 16x128 weight tile is unpacked once
+// into MFMA A operands and used for all 4 token tiles, and the fp32 accumulators of the (strip, token tile)
+// pairs stay in registers until the fused epilogue. No barrier inside a row block, so the 8 waves (2 per SIMD)
+// drift freely and one wave's MFMAs overlap the other's vector epilogue.
+// Zero points: for 2/3/4-bit codes the zero is subtracted while unpacking (c - z fits int8), so the MFMA
+// accumulates from 0 and no per-element integer work remains; 8-bit codes (stored c - 128) keep the
+// zero term zero' * (-Sxq) as the MFMA's initial accumulator.
+#include <type_traits>
+
+#include "llmoe_internal.h"
+
+namespace llmoe {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+
+constexpr int NW = TILED_WAVES;                 // waves per workgroup
+constexpr int NTHREADS = NW * 64;
+constexpr int NTILE = TILED_NTOK / 16;          // 16-token tiles per chunk
+// LDS: activations [group][token][128 B] (16-byte chunk c of token n at ((c ^ (n & 7)) * 16)), then fp32 scales
+// and negated int32 sums [group][token], then the chunk's row table [token]
+constexpr int GROUP_B = TILED_NTOK * GROUP;
+constexpr int PF_SCRATCH = 1024;                // per wave: LDS target of the L2 prefetches (never read)
+__host__ __device__ constexpr int lds_bytes_for(int K) {
+    return (K / GROUP) * (GROUP_B + TILED_NTOK * 8) + TILED_NTOK * 4 + NW * PF_SCRATCH;
+}
+constexpr int LDS_BYTES = lds_bytes_for(2048);
+
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+// The weight data of one strip-superblock held by one lane, split by when it can be refilled with the next
+// superblock: codes (BITS dwordx4; the 3-bit high plane lives in Late) and the fp16 scales of tiles 0-1 are
+// refilled group by group as soon as a tile has been unpacked; the scales of tiles 2-3, the zeros and the 3-bit
+// high plane serve all four tiles and are double-buffered a superblock ahead.
+template <int BITS>
+struct Codes {
+    static constexpr int N = BITS == 3 ? 2 : BITS;
+    u4 c[N];
+    u4 s0;          // fp16 scales [tile 0-1][rows 4q .. 4q+3]
+};
+struct Late {
+    u4 s1;          // fp16 scales [tile 2-3][rows 4q .. 4q+3]
+    u4 z;           // zeros: BITS < 8 the lane's A-operand row (byte r%4 of dword tile), 8-bit its 4 output rows
+    u4 hi;          // 3-bit high plane
+};
+
+template <int BITS>
+__device__ __forceinline__ void load_code(const uint8_t* p, int lane, int i, Codes<BITS>& r) {
+    r.c[i] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p + i * 1024) + lane);
+}
+template <int BITS>
+__device__ __forceinline__ void load_s0(const uint8_t* p, int lane, Codes<BITS>& r) {
+    r.s0 = *reinterpret_cast<const u4*>(p + BITS * 1024 + 32 * (lane >> 4));
+}
+template <int BITS>
+__device__ __forceinline__ void load_late(const uint8_t* p, int lane, Late& r) {
+    const uint8_t* m = p + BITS * 1024;
+    r.s1 = *reinterpret_cast<const u4*>(m + 32 * (lane >> 4) + 16);
+    r.z = *reinterpret_cast<const u4*>(m + 128 + 16 * (BITS == 8 ? (lane >> 4) : ((lane & 15) >> 2)));
+    if constexpr (BITS == 3) r.hi = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p + 2 * 1024) + lane);
+}
+
+// A operand dwords of tile tau (D[0..3]: columns 0..63, D[4..7]: 64..127), zero subtracted for BITS < 8:
+// (c | 0x80) - z per byte never borrows across bytes (c + 128 - z > 0), and ^ 0x80 turns the biased byte into
+// the two's complement of c - z.
+template <int BITS>
+__device__ __forceinline__ void unpack_a(const Codes<BITS>& r, const Late& lt, int tau, int lane, uint32_t (&D)[8]) {
+    if constexpr (BITS == 8) {
+        const u4& a = r.c[2 * tau];
+        const u4& b = r.c[2 * tau + 1];
+        D[0] = a.x; D[1] = a.y; D[2] = a.z; D[3] = a.w;
+        D[4] = b.x; D[5] = b.y; D[6] = b.z; D[7] = b.w;
+    } else {
+        if constexpr (BITS == 2 || BITS == 3) {
+            const u4& u = r.c[tau >> 1];
+            const uint32_t p0 = (tau & 1) ? u.z : u.x, p1 = (tau & 1) ? u.w : u.y;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                D[s] = (p0 >> (2 * s)) & 0x03030303u;
+                D[4 + s] = (p1 >> (2 * s)) & 0x03030303u;
+            }
+            if constexpr (BITS == 3) {
+                const uint32_t h = lt.hi[tau];
+#pragma unroll
+                for (int s = 0; s < 8; ++s) {
+                    const uint32_t hb = s >= 2 ? (h >> (s - 2)) : (h << (2 - s));
+                    D[s] |= hb & 0x04040404u;
+                }
+            }
+        } else {
+            const u4& u = r.c[tau];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                D[2 * m] = u[m] & 0x0F0F0F0Fu;
+                D[2 * m + 1] = (u[m] >> 4) & 0x0F0F0F0Fu;
+            }
+        }
+        const uint32_t z = (lt.z[tau] >> (8 * (lane & 3))) & 0xFFu;
+        const uint32_t zb = z * 0x01010101u;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) D[s] = ((D[s] | 0x80808080u) - zb) ^ 0x80808080u;
+    }
+}
+
+// refill, after tile tau of a superblock has been unpacked, the code / scale registers only tile tau used with
+// the next superblock at p
+template <int BITS, int TAU>
+__device__ __forceinline__ void refill_after(const uint8_t* p, int lane, Codes<BITS>& r) {
+    if constexpr (BITS == 8) {
+        load_code<BITS>(p, lane, 2 * TAU, r);
+        load_code<BITS>(p, lane, 2 * TAU + 1, r);
+    } else if constexpr (BITS == 4) {
+        load_code<BITS>(p, lane, TAU, r);
+    } else if constexpr (TAU & 1) {
+        load_code<BITS>(p, lane, TAU >> 1, r);
+    }
+    if constexpr (TAU == 1) load_s0<BITS>(p, lane, r);
+}
+
+__device__ __forceinline__ float mul_f16_f32(uint32_t packed, int hi, float x) {
+    float r;
+    if (hi) asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(x), "v"(-0.0f));
+    else asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(x), "v"(-0.0f));
+    return r;
+}
+
+// Pull 1 KiB (64 lanes x 16 B at p + 16 lane) into the L2 cache ahead of its register loads: an LDS-DMA load into
+// a per-wave scratch area of LDS that nothing reads. It holds no registers, so the prefetch can run superblocks
+// ahead of the register stream; the compiler does not see it, and its own wait counts stay conservative (the
+// hardware counter only ever holds more outstanding loads than the compiler assumes).
+__device__ __forceinline__ void l2_prefetch_kb(const uint8_t* p, uint32_t lds_scratch, int lane) {
+    const void* g = p + 16 * lane;
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_scratch)
+                 : "memory", "m0");
+}
+
+// prefetch one strip-superblock (codes and group parameters) of BITS-bit codes
+template <int BITS>
+__device__ __forceinline__ void prefetch_sb(const uint8_t* p, uint32_t lds_scratch, int lane) {
+#pragma unroll
+    for (int i = 0; i < BITS; ++i) l2_prefetch_kb(p + i * 1024, lds_scratch, lane);
+    l2_prefetch_kb(p + BITS * 1024 - 832, lds_scratch, lane);   // the 1 KiB ending with the 192 B of parameters
+}
+
+// The chunk's activations for the whole reduction -> LDS (all threads; rows of absent tokens are zero, so their
+// MFMA columns are zero). The chunk's row indices go through a small LDS table first, so that every thread then
+// issues all of its activation loads back to back. Returns after the workgroup barrier.
+template <int K>
+__device__ __forceinline__ void stage_chunk(const GemmArgs& a, const Item& it, uint8_t* lds) {
+    constexpr int G = K / GROUP, CH = K / 16, PER = TILED_NTOK * CH / NTHREADS;
+    constexpr int PS = (G * TILED_NTOK + NTHREADS - 1) / NTHREADS;
+    static_assert(PER * NTHREADS == TILED_NTOK * CH, "staging split");
+    const int tid = threadIdx.x;
+    float* ss = reinterpret_cast<float*>(lds + G * GROUP_B);
+    int* sq = reinterpret_cast<int*>(ss + G * TILED_NTOK);
+    int* rowtab = sq + G * TILED_NTOK;
+    if (tid < TILED_NTOK)
+        rowtab[tid] = tid < it.ntok ? (a.slot_token ? a.slot_token[it.slot0 + tid] : it.slot0 + tid) : -1;
+    __syncthreads();
+    u4 v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int idx = tid + NTHREADS * i, n = idx / CH, c = idx % CH;
+        const int row = rowtab[n];
+        v[i] = row >= 0 ? *reinterpret_cast<const u4*>(a.xq + size_t(row) * K + 16 * c) : u4{0u, 0u, 0u, 0u};
+    }
+    float sv[PS];
+    int qv[PS];
+#pragma unroll
+    for (int i = 0; i < PS; ++i) {
+        const int idx = tid + NTHREADS * i, n = idx / G, g = idx % G;
+        const int row = idx < G * TILED_NTOK ? rowtab[n] : -1;
+        sv[i] = row >= 0 ? a.xs[size_t(row) * G + g] : 0.0f;
+        qv[i] = row >= 0 ? -a.xsum[size_t(row) * G + g] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int idx = tid + NTHREADS * i, n = idx / CH, c = idx % CH, g = c >> 3, c16 = c & 7;
+        *reinterpret_cast<u4*>(lds + g * GROUP_B + n * GROUP + ((c16 ^ (n & 7)) << 4)) = v[i];
+    }
+#pragma unroll
+    for (int i = 0; i < PS; ++i) {
+        const int idx = tid + NTHREADS * i, n = idx / G, g = idx % G;
+        if (idx < G * TILED_NTOK) {
+            ss[g * TILED_NTOK + n] = sv[i];
+            sq[g * TILED_NTOK + n] = qv[i];
+        }
+    }
+    __syncthreads();
+}
+
+// One row block: wave w computes strips (rb * NW + w) * S .. + S - 1 for the chunk staged in LDS.
+// L2 prefetch distance in steps (one step = one superblock of the wave's strips, row blocks in sequence)
+constexpr int PF_STEPS = 2;
+
+template <int BITS, int MODE>
+__device__ __forceinline__ void prefetch_step(const GemmArgs& a, const Item& it, int rb, int sb, uint32_t scratch) {
+    constexpr int NSB = MODE == GEMM_DOWN ? 1 : 4, S = tiled_spw(BITS);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint8_t* mat = a.base + a.off[it.expert];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+        prefetch_sb<BITS>(mat + (size_t((rb * NW + wave) * S + s) * NSB + sb) * sb_bytes(BITS), scratch, lane);
+}
+
+template <int BITS, int MODE>
+__device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it, const uint8_t* lds, int rb,
+                                               int rb_end, uint32_t scratch) {
+    constexpr bool DOWN = MODE == GEMM_DOWN;
+    constexpr int NSB = DOWN ? 1 : 4, K = NSB * SB_K, G = K / GROUP;
+    constexpr int S = tiled_spw(BITS);
+    constexpr size_t SBB = sb_bytes(BITS);
+    const int lane = threadIdx.x & 63, q = lane >> 4, col = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int strip0 = (rb * NW + wave) * S;
+    const uint8_t* mat = a.base + a.off[it.expert];
+    auto sbp = [&](int s, int sb) { return mat + (size_t(strip0 + s) * NSB + sb) * SBB; };
+    const float* ss = reinterpret_cast<const float*>(lds + G * GROUP_B);
+    const int* sq = reinterpret_cast<const int*>(ss + G * TILED_NTOK);
+
+    Codes<BITS> cd[S];
+    Late lt[2][S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+        for (int i = 0; i < Codes<BITS>::N; ++i) load_code<BITS>(sbp(s, 0), lane, i, cd[s]);
+        load_s0<BITS>(sbp(s, 0), lane, cd[s]);
+        load_late<BITS>(sbp(s, 0), lane, lt[0][s]);
+        if constexpr (NSB > 1) load_late<BITS>(sbp(s, 1), lane, lt[1][s]);
+    }
+    float acc[S][NTILE][4];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int nt = 0; nt < NTILE; ++nt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[s][nt][v] = 0.0f;
+
+    static_for<0, G>([&](auto gc) {
+        constexpr int g = decltype(gc)::value, sb = g / 4, tau = g % 4;
+        const uint8_t* bg = lds + g * GROUP_B;
+        if constexpr (tau == 0) {   // L2 prefetch PF_STEPS superblocks ahead, across row blocks
+            constexpr int t = sb + PF_STEPS;
+            const int prb = rb + t / NSB;
+            if (prb < rb_end) prefetch_step<BITS, MODE>(a, it, prb, t % NSB, scratch);
+        }
+        v4i A0[S], A1[S];
+        uint32_t swp[S][2];
+        int zz[S][4];
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const Late& l = lt[sb % 2][s];
+            uint32_t Dw[8];
+            unpack_a<BITS>(cd[s], l, tau, lane, Dw);
+            A0[s] = v4i{int(Dw[0]), int(Dw[1]), int(Dw[2]), int(Dw[3])};
+            A1[s] = v4i{int(Dw[4]), int(Dw[5]), int(Dw[6]), int(Dw[7])};
+            const u4& sv = tau < 2 ? cd[s].s0 : l.s1;
+            swp[s][0] = sv[(tau & 1) * 2];
+            swp[s][1] = sv[(tau & 1) * 2 + 1];
+            if constexpr (BITS == 8) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) zz[s][v] = int((l.z[tau] >> (8 * v)) & 0xFFu) - 128;
+            }
+            // registers tile tau alone used: refill with the next superblock; after the last tile the
+            // superblock-wide registers take the superblock after next
+            if constexpr (sb + 1 < NSB) refill_after<BITS, tau>(sbp(s, sb + 1), lane, cd[s]);
+            if constexpr (tau == 3 && sb + 2 < NSB) load_late<BITS>(sbp(s, sb + 2), lane, lt[sb % 2][s]);
+        }
+        // software pipeline over the token tiles: the MFMAs of tile nt are issued before the fp32 epilogue of
+        // tile nt-1, and the B operands are read one tile ahead
+        auto bptr = [&](int nt, int half) {
+            const int n = nt * 16 + col;
+            return reinterpret_cast<const v4i*>(bg + n * GROUP + (((q + 4 * half) ^ (n & 7)) << 4));
+        };
+        v4i Cp[S];
+        float xsp = 0.0f;
+        v4i Bn0 = *bptr(0, 0), Bn1 = *bptr(0, 1);
+        float xsnext = ss[g * TILED_NTOK + col];
+        int nsnext = 0;
+        if constexpr (BITS == 8) nsnext = sq[g * TILED_NTOK + col];
+        static_for<0, NTILE + 1>([&](auto tc) {
+            constexpr int nt = decltype(tc)::value;
+            v4i Cc[S];
+            float xsn = 0.0f;
+            if constexpr (nt < NTILE) {
+                const v4i B0 = Bn0, B1 = Bn1;
+                xsn = xsnext;
+                const int nsum = nsnext;
+                if constexpr (nt + 1 < NTILE) {
+                    Bn0 = *bptr(nt + 1, 0);
+                    Bn1 = *bptr(nt + 1, 1);
+                    xsnext = ss[g * TILED_NTOK + (nt + 1) * 16 + col];
+                    if constexpr (BITS == 8) nsnext = sq[g * TILED_NTOK + (nt + 1) * 16 + col];
+                }
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    if constexpr (BITS == 8)
+                        Cc[s] = v4i{__mul24(zz[s][0], nsum), __mul24(zz[s][1], nsum), __mul24(zz[s][2], nsum),
+                                    __mul24(zz[s][3], nsum)};
+                    else
+                        Cc[s] = v4i{0, 0, 0, 0};
+                    Cc[s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0[s], B0, Cc[s], 0, 0, 0);
+                }
+#pragma unroll
+                for (int s = 0; s < S; ++s) Cc[s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1[s], B1, Cc[s], 0, 0, 0);
+            }
+            if constexpr (nt > 0) {
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        acc[s][nt - 1][v] = __builtin_fmaf(mul_f16_f32(swp[s][v >> 1], v & 1, xsp), float(Cp[s][v]),
+                                                           acc[s][nt - 1][v]);
+                    // materialise the tile's accumulators here: otherwise the compiler defers the fp32 chains
+                    // and keeps every tile's MFMA results live
+                    asm volatile("" : "+v"(acc[s][nt - 1][0]), "+v"(acc[s][nt - 1][1]), "+v"(acc[s][nt - 1][2]),
+                                 "+v"(acc[s][nt - 1][3]));
+                }
+            }
+            if constexpr (nt < NTILE) {
+#pragma unroll
+                for (int s = 0; s < S; ++s) Cp[s] = Cc[s];
+                xsp = xsn;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    });
+
+    // fused epilogue
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int strip = strip0 + s;
+#pragma unroll
+        for (int nt = 0; nt < NTILE; ++nt) {
+            const int n = nt * 16 + col;
+            if (n < it.ntok) {
+                const int slot = it.slot0 + n;
+                if constexpr (MODE == GEMM_GATE_UP) {
+                    const uint32_t z0 = f32_to_f16_bits(silu_f32(acc[s][nt][0]) * acc[s][nt][1]);
+                    const uint32_t z1 = f32_to_f16_bits(silu_f32(acc[s][nt][2]) * acc[s][nt][3]);
+                    *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
+                } else {
+                    const float w = a.slot_weight[slot];
+                    *reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q) =
+                        make_float4(w * acc[s][nt][0], w * acc[s][nt][1], w * acc[s][nt][2], w * acc[s][nt][3]);
+                }
+            }
+        }
+    }
+}
+
+template <int BITS, int MODE>
+__device__ __forceinline__ void tiled_body(const GemmArgs& a, const Item& it, uint8_t* lds) {
+    constexpr int K = MODE == GEMM_DOWN ? 512 : 2048;
+    constexpr int NSB = K / SB_K;
+    const int rb0 = it.rb & 0xFFFF, nrb = it.rb >> 16;
+    typedef __attribute__((address_space(3))) uint8_t* lds_p;
+    const uint32_t scratch = __builtin_amdgcn_readfirstlane(
+        uint32_t(size_t((lds_p)(lds + lds_bytes_for(K) - NW * PF_SCRATCH + (threadIdx.x >> 6) * PF_SCRATCH))));
+    // the first PF_STEPS steps of the wave's stream, before the activations are staged
+#pragma unroll
+    for (int t = 0; t < PF_STEPS; ++t)
+        if (rb0 + t / NSB < rb0 + nrb) prefetch_step<BITS, MODE>(a, it, rb0 + t / NSB, t % NSB, scratch);
+    stage_chunk<K>(a, it, lds);
+    for (int rb = rb0; rb < rb0 + nrb; ++rb) tiled_rowblock<BITS, MODE>(a, it, lds, rb, rb0 + nrb, scratch);
+}
+
+template <int MODE>
+__global__ void __launch_bounds__(NTHREADS) tiled_gemm(GemmArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int n = *a.n_items;
+    for (int u = blockIdx.x; u < n; u += gridDim.x) {
+        const Item it = a.items[u];
+        const int bits = a.bits[it.expert];
+#ifdef TILED_ONLY
+        tiled_body<TILED_ONLY, MODE>(a, it, lds);
+#else
+        if (bits == 2) tiled_body<2, MODE>(a, it, lds);
+        else if (bits == 3) tiled_body<3, MODE>(a, it, lds);
+        else if (bits == 4) tiled_body<4, MODE>(a, it, lds);
+        else tiled_body<8, MODE>(a, it, lds);
+#endif
+        __syncthreads();   // the next unit re-stages the activations
+    }
+}
+
+template <int MODE>
+const void* kptr() { return reinterpret_cast<const void*>(&tiled_gemm<MODE>); }
+
+template <int MODE>
+hipError_t launch_t(const GemmArgs& a, hipStream_t st) {
+    static int grid = 0;
+    if (!grid) {
+        int dev = 0, cus = 0, per_cu = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kptr<MODE>(), NTHREADS, lds_bytes_for(MODE == GEMM_DOWN ? 512 : 2048));
+        if (e != hipSuccess) return e;
+        grid = cus * (per_cu > 0 ? per_cu : 1);
+    }
+    tiled_gemm<MODE><<<grid, NTHREADS, lds_bytes_for(MODE == GEMM_DOWN ? 512 : 2048), st>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t tiled_setup() {
+    hipError_t e = hipFuncSetAttribute(kptr<GEMM_GATE_UP>(), hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+    if (e == hipSuccess) e = hipFuncSetAttribute(kptr<GEMM_DOWN>(), hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+    return e;
+}
+
+hipError_t launch_tiled_gemm(int mode, const GemmArgs& a, hipStream_t st) {
+    if (mode == GEMM_GATE_UP) return launch_t<GEMM_GATE_UP>(a, st);
+    if (mode == GEMM_DOWN) return launch_t<GEMM_DOWN>(a, st);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace llmoe

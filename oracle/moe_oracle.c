@@ -120,8 +120,6 @@ size_t orc_matrix_bytes(int R, int K, int bits) {
 static inline int tile_row(int lane, int r) { return (lane >> 2) + 8 * (r & 1); }
 static inline int tile_col(int lane, int j, int r, int b) { return 32 * j + 16 * (r >> 1) + 4 * (lane & 3) + b; }
 
-static inline void put32(uint8_t* p, uint32_t v) { memcpy(p, &v, 4); }
-static inline uint32_t get32(const uint8_t* p) { uint32_t v; memcpy(&v, p, 4); return v; }
 
 void orc_pack_i8(const uint8_t* codes, const uint16_t* scale, const uint8_t* zero, int R, int K, int bits,
                  uint8_t* out) {
@@ -353,19 +351,13 @@ void orc_group_products(const uint8_t* codes, const uint8_t* zero, int R, int K,
         }
 }
 
-/* fp32 epilogue of one row, engine/moe_i8.cu:377-383, which accumulates sum_g scale_w * scale_x * P_g in group
- * order. This build fixes the order as: per superblock of 4 groups (512 columns) an fma chain from 0,
- *   part_b = fma(scale_w[r, g] * scale_x[g], float(P[r, g]), part_b)     g = 4b .. 4b + 3 ascending
- * and the superblock partials added in order, total = ((0 + part_0) + part_1) + ... -- the same operation
- * sequence on CPU and GPU (the GPU computes the superblocks of a row in different waves). */
+/* fp32 epilogue of one row, engine/moe_i8.cu:377-383: one accumulator per (row, token), starting at 0, and
+ * for g ascending  acc = fma(scale_w[r, g] * scale_x[g], float(P[r, g]), acc)  -- the same operation sequence
+ * on CPU and GPU (the product of the two scales rounded to fp32, then one fused multiply-add per group). */
 static inline float row_epilogue(const int32_t* P, const uint16_t* sw, const float* sx, int G) {
-    float total = 0.0f;
-    for (int b = 0; b < G / 4; ++b) {
-        float part = 0.0f;
-        for (int g = 4 * b; g < 4 * b + 4; ++g) part = fmaf(orc_f16_to_f32(sw[g]) * sx[g], (float)P[g], part);
-        total = total + part;
-    }
-    return total;
+    float acc = 0.0f;
+    for (int g = 0; g < G; ++g) acc = fmaf(orc_f16_to_f32(sw[g]) * sx[g], (float)P[g], acc);
+    return acc;
 }
 
 /* FWHT-512 in fp32, Sylvester order: stages h = 1, 2, ..., 256, butterfly (a, b) -> (a + b, a - b) on indices

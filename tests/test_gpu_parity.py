@@ -143,7 +143,7 @@ def check_full(G, r, T, K, shared, tokens=None):
     (1, "mixed", True, 256),
     (45, "mixed", True, 48),     # ragged last block
     (96, 8, True, 256),
-    (200, "mixed", True, 48),    # NT = 2 / 4 items
+    (200, "mixed", True, 48),    # tiled units for the shared expert and the pool's busiest experts
 ])
 def test_layer_forward_matches_oracle(gpu, T, mix, shared, pool):
     say(f"[layer] T={T} mix={mix} shared={shared} pool={pool}")
@@ -173,6 +173,29 @@ def test_logits_routing(gpu, kind):
     r = oracle.Layer(L).forward(x, logits=lg, C=256)
     check_full(G, r, T, 8, True)
     assert np.array_equal(out.view(np.uint32), r["out"].view(np.uint32))
+    G.close()
+
+
+@pytest.mark.parametrize("T,mix,kind", [
+    (512, "mixed", "skewed"),    # 16 hot experts take half the slots: multi-chunk tiled units at every width
+    (300, 8, "skewed"),          # 8-bit tiled units (zero term on the MFMA accumulator), ragged chunks
+    (256, 2, "zipf"),
+    (384, 4, "zipf"),
+])
+def test_tiled_units_bit_exact(gpu, T, mix, kind):
+    """Experts with more than TILED_MIN slots run the tiled GEMM; every stage bit-exact against the oracle."""
+    say(f"[tiled] T={T} mix={mix} {kind}")
+    L = layer_for(mix, True, seed=61)
+    lg = synth.logits_zipf(T + 1, T) if kind == "zipf" else synth.logits_skewed(T + 1, T)
+    G = make_gpu_layer(L, 256, max_tokens=T)
+    # (outlier channels only with the 2/3/4-bit mix: random 8-bit codes around random zeros would overflow fp16 Z)
+    x = synth.make_x(500 + T, T, outlier_frac=0.01 if mix == "mixed" else 0.0)
+    out = run_layer(G, x, gpu, logits=lg)
+    assert np.isfinite(r_z := G.read("Z", (T * 9, 512), np.uint16).view(np.float16)).all(), "Z overflowed fp16"
+    r = oracle.Layer(L).forward(x, logits=lg, C=256)
+    assert (r["count"] > 40).sum() >= 8, "the case must exercise tiled units"
+    check_full(G, r, T, 8, True)
+    assert np.array_equal(out.view(np.uint32), r["out"].view(np.uint32)), "combine not bit-exact"
     G.close()
 
 
