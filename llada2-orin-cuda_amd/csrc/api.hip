@@ -63,6 +63,8 @@ struct llmoe_layer {
     float* part = nullptr;
     int32_t* topk = nullptr; float* topw = nullptr;
     uint32_t* mask = nullptr; int32_t* bpre = nullptr;
+    float* sig = nullptr;                                                          // decode routing scratch
+    uint32_t* blockmax = nullptr; uint32_t* tmask = nullptr;                      // zero between calls
     int32_t* count = nullptr; int32_t* start = nullptr;
     Item* units_gu = nullptr; Item* units_dn = nullptr; int* n_units = nullptr;   // streamed GEMM work units
     Item* tunits_gu = nullptr; Item* tunits_dn = nullptr;                          // tiled GEMM work units
@@ -265,6 +267,14 @@ int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t bl
     ALLOC(L->topw, Tm * K);
     ALLOC(L->mask, nbm * E);
     ALLOC(L->bpre, nbm * E);
+    ALLOC(L->sig, size_t(d.block) * E);
+    ALLOC(L->blockmax, E);
+    ALLOC(L->tmask, E);
+
+    if (hipMemset(L->blockmax, 0, E * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(L->tmask, 0, E * sizeof(uint32_t)) != hipSuccess || 
+        hipDeviceSynchronize() != hipSuccess)
+        return bail(fail(LLMOE_EHIP, "workspace initialisation"));
     ALLOC(L->count, E);
     ALLOC(L->start, E);
     L->items_cap = E + (Tm * K + 15) / 16 + (Tm + 15) / 16 + 2;
@@ -305,19 +315,20 @@ int llmoe_quantize_a8(const float* x, int rows, int cols, int8_t* q, float* s, i
     return LLMOE_OK;
 }
 
-int llmoe_route(llmoe_layer* L, const float* x, const float* logits, int T, llmoe_stream stream) {
-    if (int rc = check_layer(L)) return rc;
-    if (int rc = check_T(L, T)) return rc;
-    if ((x == nullptr) == (logits == nullptr)) return fail(LLMOE_EINVAL, "exactly one of x and logits must be given");
+}  // extern "C"
+
+namespace {
+// routing; with quant set (and x given) the router kernel also writes the A8 of x into the layer workspace
+int route_impl(llmoe_layer* L, const float* x, const float* logits, int T, hipStream_t st, bool quant) {
     const auto& d = L->d;
-    const hipStream_t st = static_cast<hipStream_t>(stream);
     L->routed_T = -1;
     const float* part = logits;
     int nchunks = 1;
     if (x) {
         if (!L->router_w) return fail(LLMOE_EINVAL, "layer created without a router matrix");
         L->mark(LLMOE_STAGE_ROUTER, false, st);
-        HIPCHECK(launch_router_logits(x, L->router_w, T, d.hidden, d.n_experts, L->part, st));
+        HIPCHECK(launch_router_logits(x, L->router_w, T, d.hidden, d.n_experts, L->part, quant ? L->xq : nullptr,
+                                      quant ? L->xs : nullptr, quant ? L->xsum : nullptr, st));
         L->mark(LLMOE_STAGE_ROUTER, true, st);
         part = L->part;
         nchunks = ROUTER_KC;
@@ -326,10 +337,10 @@ int llmoe_route(llmoe_layer* L, const float* x, const float* logits, int T, llmo
     if (T <= d.block) {   // one routing block (a decode step): route, plan and place in one workgroup
         choose_items(L, T);
         if (size_t(L->max_items) > L->items_cap) return fail(LLMOE_EINVAL, "item capacity exceeded");
-        HIPCHECK(launch_route_dispatch(part, nchunks, L->bias, T, d.n_experts, d.top_k, d.pool, d.block,
-                                       d.routed_scale, L->topk, L->topw, L->mask, d.has_shared, L->ntok, L->bits_d,
-                                       L->count, L->start, L->units_gu, L->units_dn, L->n_units, L->slot_token,
-                                       L->slot_weight, L->tok_slots, st));
+        HIPCHECK(launch_decode_route(part, nchunks, L->bias, T, d.n_experts, d.top_k, d.pool, d.routed_scale, L->sig,
+                                     L->topk, L->topw, L->blockmax, L->tmask, d.has_shared, L->bits_d,
+                                     L->count, L->start, L->units_gu, L->units_dn, L->n_units, L->slot_token,
+                                     L->slot_weight, L->tok_slots, st));
         L->mark(LLMOE_STAGE_ROUTE, true, st);
         L->routed_T = T;
         return LLMOE_OK;
@@ -338,6 +349,16 @@ int llmoe_route(llmoe_layer* L, const float* x, const float* logits, int T, llmo
                           L->topw, L->mask, st));
     L->mark(LLMOE_STAGE_ROUTE, true, st);
     return plan_and_place(L, L->topk, L->topw, T, st);
+}
+}  // namespace
+
+extern "C" {
+
+int llmoe_route(llmoe_layer* L, const float* x, const float* logits, int T, llmoe_stream stream) {
+    if (int rc = check_layer(L)) return rc;
+    if (int rc = check_T(L, T)) return rc;
+    if ((x == nullptr) == (logits == nullptr)) return fail(LLMOE_EINVAL, "exactly one of x and logits must be given");
+    return route_impl(L, x, logits, T, static_cast<hipStream_t>(stream), false);
 }
 
 int llmoe_dispatch(llmoe_layer* L, const int32_t* topk, const float* topw, int T, llmoe_stream stream) {
@@ -410,10 +431,14 @@ int llmoe_layer_forward(llmoe_layer* L, const float* x, const float* logits, int
     if (int rc = check_layer(L)) return rc;
     if (int rc = check_T(L, T)) return rc;
     if (!x || !out) return fail(LLMOE_EINVAL, "null argument");
-    L->mark(LLMOE_STAGE_QUANT, false, static_cast<hipStream_t>(stream));
-    if (int rc = llmoe_quantize_a8(x, T, L->d.hidden, L->xq, L->xs, L->xsum, stream)) return rc;
-    L->mark(LLMOE_STAGE_QUANT, true, static_cast<hipStream_t>(stream));
-    if (int rc = llmoe_route(L, logits ? nullptr : x, logits, T, stream)) return rc;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (logits || !L->router_w) {   // A8 on its own; with the router, its kernel quantises x on the way
+        L->mark(LLMOE_STAGE_QUANT, false, st);
+        if (int rc = llmoe_quantize_a8(x, T, L->d.hidden, L->xq, L->xs, L->xsum, stream)) return rc;
+        L->mark(LLMOE_STAGE_QUANT, true, st);
+    }
+    if (!logits && !L->router_w) return fail(LLMOE_EINVAL, "layer created without a router matrix");
+    if (int rc = route_impl(L, logits ? nullptr : x, logits, T, st, logits == nullptr)) return rc;
     return llmoe_experts(L, L->xq, L->xs, L->xsum, T, out, stream);
 }
 

@@ -151,15 +151,19 @@ hipError_t launch_quant_a8(const float* x, int rows, int cols, int8_t* q, float*
 hipError_t launch_fwht_a8(const uint16_t* Z, int nslots, int8_t* q, float* s, int* sum, hipStream_t st);
 hipError_t launch_combine(const float* Y, const int* tok_slots, int T, int H, int kk, int K1, float* out,
                           hipStream_t st);
-hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, int E, float* part, hipStream_t st);
+// router logits partials; with q != nullptr also the A8 of x (q, qs, qsum as launch_quant_a8), H = 2048
+hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, int E, float* part, int8_t* q,
+                                float* qs, int* qsum, hipStream_t st);
 hipError_t launch_route(const float* part, int nchunks, const float* bias, int T, int E, int K, int C, int block,
                         float rscale, int32_t* topk, float* topw, uint32_t* mask, hipStream_t st);
-// single routing block (T <= block): route + plan + place in one workgroup
-hipError_t launch_route_dispatch(const float* part, int nchunks, const float* bias, int T, int E, int K, int C,
-                                 int block, float rscale, int32_t* topk, float* topw, uint32_t* mask, int has_shared,
-                                 int ntok, const int8_t* bits, int32_t* count, int32_t* start, Item* units_gu,
-                                 Item* units_dn, int* n_units, int32_t* slot_token, float* slot_weight,
-                                 int32_t* tok_slots, hipStream_t st);
+// decode step (T <= 32, one routing block): [scores and pool keys (pool < E)], selection in ceil(T/8)
+// workgroups, then one workgroup builds the slots and work units (streamed, 16 slots per item). blockmax / tmask
+// [E] must be zero on entry and are zero again on exit. sig: [T, E] scratch.
+hipError_t launch_decode_route(const float* part, int nchunks, const float* bias, int T, int E, int K, int C,
+                               float rscale, float* sig, int32_t* topk, float* topw, uint32_t* blockmax,
+                               uint32_t* tmask, int has_shared, const int8_t* bits, int32_t* count, int32_t* start,
+                               Item* units_gu, Item* units_dn, int* n_units, int32_t* slot_token, float* slot_weight,
+                               int32_t* tok_slots, hipStream_t st);
 hipError_t launch_masks(const int32_t* topk, int T, int E, int K, int block, uint32_t* mask, hipStream_t st);
 // work units: streamed units_gu / units_dn (n_units[0] / [1], items of <= ntok slots), tiled tunits_gu /
 // tunits_dn (n_units[2] / [3]) for experts with more than TILED_MIN slots when `tiled` is set

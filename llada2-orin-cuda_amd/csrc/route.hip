@@ -11,52 +11,99 @@ constexpr int MAXB = 32;    // tokens per routing block (one 32-bit token mask p
 constexpr int MAXE = 256;   // experts (one thread each)
 
 // logits partial c: fma chain over k = c H/8 .. (c+1) H/8 - 1 ascending from 0 (the summation order is fixed so
-// the CPU checker reproduces it). Workgroup tile: 32 tokens x 64 experts of one K chunk, the chunk's x and Wr
-// slices staged in LDS by one batch of loads; thread: 2 tokens x 4 experts.
-// grid (E/64, ceil(T/32), 8), 256 threads, dynamic LDS ROUTER_LDS.
+// the CPU checker reproduces it). Workgroup tile: 32 tokens x 16 experts of one K chunk, the chunk's x and Wr
+// slices staged in LDS by one batch of loads; thread: 1 token x 2 experts. grid (E/16, ceil(T/32), 8) = 128
+// workgroups at T <= 32, 256 threads, dynamic LDS ROUTER_LDS.
+// With q != nullptr the workgroups of expert slice 0 also write the A8 of their x slice (two 128-groups per
+// token, the same operations as quant_a8_kernel), so the layer input is quantised without a launch of its own.
+__device__ __forceinline__ uint32_t okey(float v) {        // order-preserving unsigned image of a float
+    const uint32_t u = __float_as_uint(v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 constexpr int RKW = 256;                                          // K per chunk (H = 2048)
-constexpr int ROUTER_LDS = (32 * (RKW + 4) + RKW * 64) * 4;
+constexpr int RXS = RKW + 4;                                      // LDS row stride of the x slice
+constexpr int ROUTER_LDS = (32 * RXS + RKW * 16) * 4;
 __global__ void __launch_bounds__(256) router_logits_kernel(const float* __restrict__ x, const float* __restrict__ Wr,
-                                                            int T, int H, int E, float* __restrict__ part) {
+                                                            int T, int H, int E, float* __restrict__ part,
+                                                            int8_t* __restrict__ q, float* __restrict__ qs,
+                                                            int* __restrict__ qsum) {
     extern __shared__ __align__(16) float rl[];
-    float* xs = rl;                       // [32][RKW + 4]
-    float* ws = rl + 32 * (RKW + 4);      // [RKW][64]
-    const int e0 = blockIdx.x * 64, t0 = blockIdx.y * 32, c = blockIdx.z, kb = c * RKW;
-    const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+    float* xs = rl;                       // [32][RXS]
+    float* ws = rl + 32 * RXS;            // [RKW][16]
+    const int e0 = blockIdx.x * 16, t0 = blockIdx.y * 32, c = blockIdx.z, kb = c * RKW;
+    const int tid = threadIdx.x;
+    float4 xv[8], wv[4];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {                                 // x: 32 x 256 floats as float4
         const int idx = tid + 256 * i, t = idx >> 6, k4 = idx & 63;
-        const float4 v = t0 + t < T ? *reinterpret_cast<const float4*>(x + size_t(t0 + t) * H + kb + 4 * k4)
-                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        *reinterpret_cast<float4*>(xs + t * (RKW + 4) + 4 * k4) = v;
+        xv[i] = t0 + t < T ? *reinterpret_cast<const float4*>(x + size_t(t0 + t) * H + kb + 4 * k4)
+                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {                                // Wr: 256 x 64 floats as float4
-        const int idx = tid + 256 * i, k = idx >> 4, e4 = idx & 15;
-        *reinterpret_cast<float4*>(ws + k * 64 + 4 * e4) =
-            *reinterpret_cast<const float4*>(Wr + size_t(kb + k) * E + e0 + 4 * e4);
+    for (int i = 0; i < 4; ++i) {                                 // Wr: 256 x 16 floats as float4
+        const int idx = tid + 256 * i, k = idx >> 2, e4 = idx & 3;
+        wv[i] = *reinterpret_cast<const float4*>(Wr + size_t(kb + k) * E + e0 + 4 * e4);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int idx = tid + 256 * i, t = idx >> 6, k4 = idx & 63;
+        *reinterpret_cast<float4*>(xs + t * RXS + 4 * k4) = xv[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int idx = tid + 256 * i, k = idx >> 2, e4 = idx & 3;
+        *reinterpret_cast<float4*>(ws + k * 16 + 4 * e4) = wv[i];
     }
     __syncthreads();
-    float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-    const float* xa = xs + (2 * ty) * (RKW + 4);
-    const float* xb = xa + (RKW + 4);
-#pragma unroll 8
-    for (int k = 0; k < RKW; ++k) {
-        const float a = xa[k], b = xb[k];
-        const float4 w = *reinterpret_cast<const float4*>(ws + k * 64 + 4 * tx);
-        const float wv[4] = {w.x, w.y, w.z, w.w};
+    const int t = tid >> 3, e2 = tid & 7;
+    float acc0 = 0.0f, acc1 = 0.0f;
+    const float* xa = xs + t * RXS;
+#pragma unroll 4
+    for (int k = 0; k < RKW; k += 4) {
+        const float4 a = *reinterpret_cast<const float4*>(xa + k);
+        const float av[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            acc[0][j] = __builtin_fmaf(a, wv[j], acc[0][j]);
-            acc[1][j] = __builtin_fmaf(b, wv[j], acc[1][j]);
+            const float2 w = *reinterpret_cast<const float2*>(ws + (k + j) * 16 + 2 * e2);
+            acc0 = __builtin_fmaf(av[j], w.x, acc0);
+            acc1 = __builtin_fmaf(av[j], w.y, acc1);
         }
     }
+    if (t0 + t < T)
+        *reinterpret_cast<float2*>(part + (size_t(c) * T + t0 + t) * E + e0 + 2 * e2) = make_float2(acc0, acc1);
+    if (q != nullptr && blockIdx.x == 0) {
+        // A8 of the slice: (token, group) pair p = tid / 4, 4 threads x 32 values each
+        const int p = tid >> 2, part4 = tid & 3, tt = p >> 1, gl = p & 1;
+        const float* v = xs + tt * RXS + gl * GROUP + part4 * 32;
+        float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int t = t0 + 2 * ty + i;
-        if (t < T)
-            *reinterpret_cast<float4*>(part + (size_t(c) * T + t) * E + e0 + 4 * tx) =
-                make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+        for (int j = 0; j < 32; ++j) m = fmaxf(m, fabsf(v[j]));
+        m = fmaxf(m, __shfl_xor(m, 1));
+        m = fmaxf(m, __shfl_xor(m, 2));
+        const float sc = fmaxf(m / 127.0f, 1e-30f);
+        int tot = 0;
+        uint32_t w[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[j] = 0u;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const int qq = int(fminf(fmaxf(__builtin_rintf(v[j] / sc), -127.0f), 127.0f));
+            tot += qq;
+            w[j >> 2] |= uint32_t(qq & 0xFF) << (8 * (j & 3));
+        }
+        tot += __shfl_xor(tot, 1);
+        tot += __shfl_xor(tot, 2);
+        if (t0 + tt < T) {
+            int8_t* dst = q + size_t(t0 + tt) * H + kb + gl * GROUP + part4 * 32;
+            *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+            *reinterpret_cast<uint4*>(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
+            if (part4 == 0) {
+                const size_t gi = size_t(t0 + tt) * (H / GROUP) + c * (RKW / GROUP) + gl;
+                qs[gi] = sc;
+                qsum[gi] = tot;
+            }
+        }
     }
 }
 
@@ -111,48 +158,6 @@ __device__ __forceinline__ void merge8(uint64_t (&k)[8], const uint64_t (&w)[8])
 __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int o) {
     const uint32_t lo = __shfl_xor(uint32_t(v), o), hi = __shfl_xor(uint32_t(v >> 32), o);
     return (uint64_t(hi) << 32) | lo;
-}
-
-// exclusive prefix sums of two per-expert values over E <= 256 experts, by wave 0 (4 experts per lane);
-// results in LDS arrays ex_a/ex_b, totals in tot[0..1]. All threads must call it (it synchronises).
-__device__ void expert_scan2(const int* va, const int* vb, int E, int* ex_a, int* ex_b, int* tot) {
-    if (threadIdx.x < 64) {
-        const int l = threadIdx.x;
-        int a[4], b[4], sa = 0, sb = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = 4 * l + j;
-            a[j] = e < E ? va[e] : 0;
-            b[j] = e < E ? vb[e] : 0;
-            sa += a[j];
-            sb += b[j];
-        }
-        int ia = sa, ib = sb;   // inclusive scan over lanes
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int ta = __shfl_up(ia, o), tb2 = __shfl_up(ib, o);
-            if (l >= o) {
-                ia += ta;
-                ib += tb2;
-            }
-        }
-        int ra = ia - sa, rb = ib - sb;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = 4 * l + j;
-            if (e < E) {
-                ex_a[e] = ra;
-                ex_b[e] = rb;
-            }
-            ra += a[j];
-            rb += b[j];
-        }
-        if (l == 63) {
-            tot[0] = ia;
-            tot[1] = ib;
-        }
-    }
-    __syncthreads();
 }
 
 // exclusive prefix sum over the NT threads of a block (Hillis-Steele in LDS); *total = the full sum
@@ -291,23 +296,27 @@ struct DispatchOut {         // written by the single-block fused route (decode)
     int* tok_slots;
 };
 
+// shared-expert unit u of a list with r row blocks per item (items of 16 slots at T K + 16 j)
+__device__ __forceinline__ void units_shared(Item* list, int u, int r, int E, int T, int K) {
+    const int j = u / r;
+    list[u] = Item{E, T * K + 16 * j, min(16, T - 16 * j), u % r};
+}
+
 constexpr int RT_THREADS = 1024;
 
 // One routing block per workgroup (engine/ops.cu:256-327, quant/s03_teacher_pass.py:132-146):
 //   logit = sum of the nchunks partials (c ascending); score = sigmoid(logit); s = score + bias;
 //   pool = top-C experts by max over the block's tokens of s, ranked (value desc, index asc) (C >= E: all);
-//   per token top-K of s in the pool, (value desc, index asc): 8 lanes per token each keep a sorted top-8 of
-//   their 32 experts, then three xor-shuffle merges give every lane the token's top-8;
+//   per token top-K of s in the pool, (value desc, index asc): 32 lanes per token each keep a sorted top-8 of
+//   their 8 experts, then five xor-shuffle merges give every lane the token's top-8;
 //   w_k = score_k / (sum_k score_k + 1e-20) * rscale, the sum in rank order.
-// Writes topk/topw [T, K] and mask[block, e] = bit t of the block's tokens that picked e. FUSED (T <= block, the
-// decode step, engine/ops.cu:333-370): the same workgroup also builds the slots and work items.
-// 1024 threads: every partial of the block is loaded in one batch.
-template <bool FUSED>
+// Writes topk/topw [T, K] and mask[block, e] = bit t of the block's tokens that picked e (the multi-block path;
+// the decode step uses score / select / dispatch below). 1024 threads: every partial of the block is loaded in
+// one batch.
 __global__ void __launch_bounds__(RT_THREADS) route_kernel(const float* __restrict__ part, int nchunks,
                                                            const float* __restrict__ bias, int T, int E, int K, int C,
                                                            int block, float rscale, int* __restrict__ topk,
-                                                           float* __restrict__ topw, uint32_t* __restrict__ mask,
-                                                           DispatchOut dout) {
+                                                           float* __restrict__ topw, uint32_t* __restrict__ mask) {
     __shared__ float sig[MAXB][MAXE + 1];
     __shared__ uint64_t key[MAXE];
     __shared__ float sbias[MAXE];
@@ -420,51 +429,243 @@ __global__ void __launch_bounds__(RT_THREADS) route_kernel(const float* __restri
     }
     __syncthreads();
     if (tid < E) mask[size_t(b) * E + tid] = tmask[tid];
-    if constexpr (FUSED) {
-        // one block: slot ranges = exclusive scan of the per-expert token counts; work units (items of <= ntok
-        // slots, split into row blocks by code width) ordered heaviest first
-        const int ns = dout.has_shared ? (T + dout.ntok - 1) / dout.ntok : 0;
-        const int sbits = dout.has_shared ? dout.bits[E] : 8;
-        if (tid < E) {
-            const int c = __popc(tmask[tid]);
-            const int b = dout.bits[tid];
-            const int nit = (c + dout.ntok - 1) / dout.ntok;
-            cnt[tid] = c;
-            nits[tid] = nit;
-            nu_gu[tid] = nit * gemm_row_blocks(false, b);
-            nu_dn[tid] = nit * gemm_row_blocks(true, b);
-            wcls[tid] = width_class(b);
-        }
-        __syncthreads();
-        expert_scan2(cnt, nits, E, sstart, ibase, tots);
-        unit_offsets(nu_gu, nu_dn, wcls, E, ns * gemm_row_blocks(false, sbits), ns * gemm_row_blocks(true, sbits),
-                     ub_gu, ub_dn, utot);
-        if (tid < E) {
-            dout.count[tid] = cnt[tid];
-            dout.start[tid] = sstart[tid];
-            emit_units(tid, cnt[tid], sstart[tid], dout.ntok, dout.bits[tid], ub_gu[tid], ub_dn[tid], dout.units_gu,
-                       dout.units_dn);
-        }
-        if (ns) emit_shared_units(E, T, K, dout.ntok, sbits, dout.units_gu, dout.units_dn);
-        if (tid == 0) {
-            dout.n_units[0] = utot[0];
-            dout.n_units[1] = utot[1];
-        }
-        __syncthreads();
-        if (owner) {
-            const int t = t0 + tl;
-            const int sl = sstart[mysel] + __popc(tmask[mysel] & ((1u << tl) - 1u));
-            dout.slot_token[sl] = t;
-            dout.slot_weight[sl] = mine / (wsum + 1e-20f) * rscale;
-            dout.tok_slots[size_t(t) * (K + 1) + sub] = sl;
-        }
-        if (tid < tb) {
-            const int t = t0 + tid;
-            if (dout.has_shared) {
-                dout.slot_token[T * K + t] = t;
-                dout.slot_weight[T * K + t] = 1.0f;
+}
+
+// ---- decode routing (one routing block, T <= block <= 32): scores, then selection + dispatch ----------------
+// The selection runs in ceil(T/8) workgroups (8 tokens each, 32 lanes per token) instead of one; the last
+// workgroup to finish (a device-scope counter) builds the slots and work units for all tokens. DecodeState is
+// zero when a call starts and the dispatching workgroup leaves it zero again.
+
+// grid T, 256 threads (thread = expert): logit = partials summed in chunk order; sig[t, e] = sigmoid(logit);
+// with the pool, blockmax[e] = max over tokens of the ordered key of sigmoid + bias
+__global__ void __launch_bounds__(256) score_kernel(const float* __restrict__ part, int nchunks,
+                                                    const float* __restrict__ bias, int T, int E, int pool_on,
+                                                    float* __restrict__ sig, uint32_t* __restrict__ blockmax) {
+    const int t = blockIdx.x, e = threadIdx.x;
+    if (e >= E) return;
+    float p[ROUTER_KC];
+#pragma unroll
+    for (int c = 0; c < ROUTER_KC; ++c) p[c] = c < nchunks ? part[(size_t(c) * T + t) * E + e] : 0.0f;
+    float l = p[0];
+#pragma unroll
+    for (int c = 1; c < ROUTER_KC; ++c)
+        if (c < nchunks) l = l + p[c];
+    const float sg = sigmoid_f32(l);
+    sig[size_t(t) * E + e] = sg;
+    if (pool_on) atomicMax(&blockmax[e], okey(sg + bias[e]));
+}
+
+struct DecodeState {
+    uint32_t* blockmax;   // [E] ordered keys of max_t (sigmoid + bias)
+    uint32_t* tmask;      // [E] bit t: token t picked the expert
+};
+
+// Slots and work units of the decode step (engine/ops.cu:333-370), one workgroup of 256 threads.
+// Slots: expert-major, token-ascending; shared slots T K + t. Units: items of 16 slots split into row blocks by
+// code width, heaviest first (the shared expert, then 8 / 4 / 3 / 2-bit experts).
+__global__ void __launch_bounds__(256) dispatch_kernel(int T, int E, int K, const int* __restrict__ topk,
+                                                       const float* __restrict__ topw, DecodeState ds, DispatchOut d) {
+    __shared__ uint32_t m_s[MAXE];
+    __shared__ int start_s[MAXE];
+    __shared__ int wt_i[4];
+    __shared__ uint64_t wt_g[4], wt_d[4];
+    __shared__ uint64_t tot_g, tot_d;
+    const int e = threadIdx.x;
+    const uint32_t m = e < E ? ds.tmask[e] : 0u;
+    if (e < E) {
+        m_s[e] = m;
+        ds.tmask[e] = 0u;
+        ds.blockmax[e] = 0u;
+    }
+    const int c = __popc(m);
+    const int bw = e < E ? d.bits[e] : 2;
+    const int nit = (c + 15) >> 4;
+    const int cls = width_class(bw);
+    const uint64_t vg = uint64_t(nit * gemm_row_blocks(false, bw)) << (16 * cls);
+    const uint64_t vd = uint64_t(nit * gemm_row_blocks(true, bw)) << (16 * cls);
+    int incl = c;
+    uint64_t ig = vg, id = vd;
+    {   // three inclusive scans over the 256 threads in one pass: wave shuffles, then the wave totals
+        const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int ui = __shfl_up(incl, o);
+            const uint64_t ug = __shfl_up(ig, o), ud = __shfl_up(id, o);
+            if (lane >= o) {
+                incl += ui;
+                ig += ug;
+                id += ud;
             }
-            dout.tok_slots[size_t(t) * (K + 1) + K] = dout.has_shared ? T * K + t : -1;
+        }
+        if (lane == 63) {
+            wt_i[w] = incl;
+            wt_g[w] = ig;
+            wt_d[w] = id;
+        }
+        __syncthreads();
+        for (int i = 0; i < w; ++i) {
+            incl += wt_i[i];
+            ig += wt_g[i];
+            id += wt_d[i];
+        }
+    }
+    if (e == 255) {
+        tot_g = ig;
+        tot_d = id;
+    }
+    const int st = incl - c;
+    if (e < E) start_s[e] = st;
+    __syncthreads();
+    const int sbits = d.has_shared ? d.bits[E] : 8;
+    const int ns = d.has_shared ? (T + 15) >> 4 : 0;
+    const int srg = gemm_row_blocks(false, sbits), srd = gemm_row_blocks(true, sbits);
+    // class bases: shared units first, then classes 0 .. 3
+    int bg = ns * srg, bd = ns * srd, og = 0, od = 0;
+    for (int k = 0; k < 4; ++k) {
+        if (k == cls) {
+            og = bg + int(((ig - vg) >> (16 * k)) & 0xFFFFu);
+            od = bd + int(((id - vd) >> (16 * k)) & 0xFFFFu);
+        }
+        bg += int((tot_g >> (16 * k)) & 0xFFFFu);
+        bd += int((tot_d >> (16 * k)) & 0xFFFFu);
+    }
+    if (e < E) {
+        d.count[e] = c;
+        d.start[e] = st;
+        const int rg = gemm_row_blocks(false, bw), rd = gemm_row_blocks(true, bw);
+        for (int j = 0; j < nit; ++j) {
+            const int s0 = st + 16 * j, n = min(16, c - 16 * j);
+            for (int r = 0; r < rg; ++r) d.units_gu[og + j * rg + r] = Item{e, s0, n, r};
+            for (int r = 0; r < rd; ++r) d.units_dn[od + j * rd + r] = Item{e, s0, n, r};
+        }
+    }
+    for (int u = e; u < ns * srg; u += 256) units_shared(d.units_gu, u, srg, E, T, K);
+    for (int u = e; u < ns * srd; u += 256) units_shared(d.units_dn, u, srd, E, T, K);
+    if (e == 0) {
+        d.n_units[0] = bg;
+        d.n_units[1] = bd;
+        d.n_units[2] = 0;
+        d.n_units[3] = 0;
+    }
+    // place every (token, k) pair
+    for (int p = e; p < T * K; p += 256) {
+        const int t = p / K;
+        const int ex = topk[p];
+        const float w = topw[p];
+        const int sl = start_s[ex] + __popc(m_s[ex] & ((1u << t) - 1u));
+        d.slot_token[sl] = t;
+        d.slot_weight[sl] = w;
+        d.tok_slots[p + t] = sl;                      // [t][k] of the [T][K + 1] table
+    }
+    if (e < T) {
+        if (d.has_shared) {
+            d.slot_token[T * K + e] = e;
+            d.slot_weight[T * K + e] = 1.0f;
+        }
+        d.tok_slots[size_t(e) * (K + 1) + K] = d.has_shared ? T * K + e : -1;
+    }
+}
+
+// grid ceil(T/8), 256 threads: pool membership (POOL: from blockmax of score_kernel), top-K of 8 tokens, routing
+// weights, token masks (engine/ops.cu:256-327, quant/s03_teacher_pass.py:132-146). Without the pool the scores
+// come straight from the router partials (summed in chunk order, as score_kernel does).
+template <bool POOL>
+__global__ void __launch_bounds__(256) select_kernel(const float* __restrict__ part, int nchunks,
+                                                     const float* __restrict__ sig, const float* __restrict__ bias,
+                                                     int T, int E, int K, int C, float rscale, int* __restrict__ topk,
+                                                     float* __restrict__ topw, DecodeState ds) {
+    __shared__ __align__(16) uint64_t key[MAXE];
+    __shared__ float sbias[MAXE];
+    __shared__ int inpool[MAXE];
+    __shared__ float sigl[8][MAXE];
+    const int tid = threadIdx.x;
+    if (tid < MAXE) {
+        sbias[tid] = tid < E ? bias[tid] : 0.0f;
+        if (POOL) key[tid] = tid < E ? (uint64_t(ds.blockmax[tid]) << 32) | uint32_t(0xFFFF - tid) : 0ull;
+    }
+    __syncthreads();
+    if (tid < E) {   // pool = the C largest keys: rank = number of larger keys
+        int rank = 0;
+        if (POOL) {
+            const uint64_t ke = key[tid];
+            const ulonglong2* k2 = reinterpret_cast<const ulonglong2*>(key);
+#pragma unroll 8
+            for (int j = 0; j < MAXE / 2; ++j) {
+                const ulonglong2 kk = k2[j];
+                rank += (kk.x > ke) + (kk.y > ke);
+            }
+        }
+        inpool[tid] = rank < C;
+    }
+    __syncthreads();
+    const int tl = tid >> 5, sub = tid & 31, t = blockIdx.x * 8 + tl;
+    const bool valid = t < T;
+    float sv[8];
+    if (valid && sub * 8 < E) {
+        if constexpr (POOL) {
+            const float4 a = *reinterpret_cast<const float4*>(sig + size_t(t) * E + sub * 8);
+            const float4 b = *reinterpret_cast<const float4*>(sig + size_t(t) * E + sub * 8 + 4);
+            sv[0] = a.x; sv[1] = a.y; sv[2] = a.z; sv[3] = a.w; sv[4] = b.x; sv[5] = b.y; sv[6] = b.z; sv[7] = b.w;
+        } else {
+            float4 p[ROUTER_KC][2];
+#pragma unroll
+            for (int c = 0; c < ROUTER_KC; ++c)
+                if (c < nchunks) {
+                    const float* pp = part + (size_t(c) * T + t) * E + sub * 8;
+                    p[c][0] = *reinterpret_cast<const float4*>(pp);
+                    p[c][1] = *reinterpret_cast<const float4*>(pp + 4);
+                }
+            float l[8] = {p[0][0].x, p[0][0].y, p[0][0].z, p[0][0].w, p[0][1].x, p[0][1].y, p[0][1].z, p[0][1].w};
+#pragma unroll
+            for (int c = 1; c < ROUTER_KC; ++c)
+                if (c < nchunks) {
+                    const float q8[8] = {p[c][0].x, p[c][0].y, p[c][0].z, p[c][0].w,
+                                         p[c][1].x, p[c][1].y, p[c][1].z, p[c][1].w};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) l[j] = l[j] + q8[j];
+                }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) sv[j] = sigmoid_f32(l[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sigl[tl][sub * 8 + j] = sv[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sv[j] = 0.0f;
+    }
+    uint64_t best[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int ex = sub * 8 + j;
+        best[j] = valid && ex < E && inpool[ex] ? sel_key(sv[j] + sbias[ex], ex) : 0ull;
+    }
+    sort8(best);
+#pragma unroll 1
+    for (int o = 1; o < 32; o <<= 1) {
+        uint64_t other[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) other[k] = shfl_xor64(best[k], o);
+        merge8(best, other);
+    }
+    if (valid) {
+        float wsum = 0.0f, mine = 0.0f;
+        int mysel = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (k < K) {
+                const int ex = key_index(best[k]);
+                const float sk = sigl[tl][ex];
+                wsum = wsum + sk;
+                if (k == sub) {
+                    mine = sk;
+                    mysel = ex;
+                }
+            }
+        }
+        if (sub < K) {
+            topk[size_t(t) * K + sub] = mysel;
+            topw[size_t(t) * K + sub] = mine / (wsum + 1e-20f) * rscale;
+            atomicOr(&ds.tmask[mysel], 1u << t);
         }
     }
 }
@@ -577,7 +778,8 @@ __global__ void __launch_bounds__(256) place_kernel(const int* __restrict__ topk
 
 }  // namespace
 
-hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, int E, float* part, hipStream_t st) {
+hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, int E, float* part, int8_t* q,
+                                float* qs, int* qsum, hipStream_t st) {
     static bool attr = false;
     if (!attr) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(router_logits_kernel),
@@ -585,28 +787,34 @@ hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, i
         if (e != hipSuccess) return e;
         attr = true;
     }
-    const dim3 grid(E / 64, (T + 31) / 32, ROUTER_KC);
-    router_logits_kernel<<<grid, 256, ROUTER_LDS, st>>>(x, Wr, T, H, E, part);
+    const dim3 grid(E / 16, (T + 31) / 32, ROUTER_KC);
+    router_logits_kernel<<<grid, 256, ROUTER_LDS, st>>>(x, Wr, T, H, E, part, q, qs, qsum);
     return hipGetLastError();
 }
 
 hipError_t launch_route(const float* part, int nchunks, const float* bias, int T, int E, int K, int C, int block,
                         float rscale, int32_t* topk, float* topw, uint32_t* mask, hipStream_t st) {
     const int nb = (T + block - 1) / block;
-    route_kernel<false><<<nb, RT_THREADS, 0, st>>>(part, nchunks, bias, T, E, K, C, block, rscale, topk, topw, mask,
-                                                   DispatchOut{});
+    route_kernel<<<nb, RT_THREADS, 0, st>>>(part, nchunks, bias, T, E, K, C, block, rscale, topk, topw, mask);
     return hipGetLastError();
 }
 
-hipError_t launch_route_dispatch(const float* part, int nchunks, const float* bias, int T, int E, int K, int C,
-                                 int block, float rscale, int32_t* topk, float* topw, uint32_t* mask, int has_shared,
-                                 int ntok, const int8_t* bits, int32_t* count, int32_t* start, Item* units_gu,
-                                 Item* units_dn, int* n_units, int32_t* slot_token, float* slot_weight,
-                                 int32_t* tok_slots, hipStream_t st) {
-    if (T > block) return hipErrorInvalidValue;
-    const DispatchOut d{has_shared, ntok, bits, count, start, units_gu, units_dn, n_units, slot_token, slot_weight,
+hipError_t launch_decode_route(const float* part, int nchunks, const float* bias, int T, int E, int K, int C,
+                               float rscale, float* sig, int32_t* topk, float* topw, uint32_t* blockmax,
+                               uint32_t* tmask, int has_shared, const int8_t* bits, int32_t* count, int32_t* start,
+                               Item* units_gu, Item* units_dn, int* n_units, int32_t* slot_token, float* slot_weight,
+                               int32_t* tok_slots, hipStream_t st) {
+    if (T > 32 || E > MAXE) return hipErrorInvalidValue;
+    const DecodeState ds{blockmax, tmask};
+    if (C < E) {
+        score_kernel<<<T, 256, 0, st>>>(part, nchunks, bias, T, E, 1, sig, blockmax);
+        select_kernel<true><<<(T + 7) / 8, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, rscale, topk, topw, ds);
+    } else {
+        select_kernel<false><<<(T + 7) / 8, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, rscale, topk, topw, ds);
+    }
+    const DispatchOut d{has_shared, 16, bits, count, start, units_gu, units_dn, n_units, slot_token, slot_weight,
                         tok_slots};
-    route_kernel<true><<<1, RT_THREADS, 0, st>>>(part, nchunks, bias, T, E, K, C, block, rscale, topk, topw, mask, d);
+    dispatch_kernel<<<1, 256, 0, st>>>(T, E, K, topk, topw, ds, d);
     return hipGetLastError();
 }
 
