@@ -191,6 +191,42 @@ def copy_calibration(torch, mib=512, reps=3):
     log(f"[bench] copy calibration: {reps} copies of {mib} MiB")
 
 
+def prefill_config(llmoe, synth, torch, name, T, mix, shared, pool, logits_kind, steps, warmup, nlayers=2,
+                   outliers=0.0):
+    """One layer of T tokens (configs 2 and 4): a step is one full layer pass; the layers cycle so their weights
+    stream from HBM. logits_kind: None (router x Wr), "uniform" (random logits), "skewed" (16 experts take half
+    of the slots)."""
+    dev = torch.device("cuda:0")
+    Ls = [synth.make_layer(300 + 7 * i, mix=mix, shared=shared, zero_bias=logits_kind is not None)
+          for i in range(nlayers)]
+    Gs = [make_gpu_layer(llmoe, L, pool, T) for L in Ls]
+    x = torch.from_numpy(synth.make_x(31, T, outlier_frac=outliers)).to(dev)
+    lgs = [None] * nlayers
+    if logits_kind == "uniform":
+        lgs = [torch.from_numpy(np.random.default_rng(40 + i).standard_normal((T, E)).astype(np.float32)).to(dev)
+               for i in range(nlayers)]
+    elif logits_kind == "skewed":
+        lgs = [torch.from_numpy(synth.logits_skewed(40 + i, T)).to(dev) for i in range(nlayers)]
+    out = torch.empty((T, H), dtype=torch.float32, device=dev)
+    fn = lambda i: Gs[i % nlayers].forward(x, lgs[i % nlayers], out=out)  # noqa: E731
+    dt = time_steps(fn, steps, warmup)
+    for i in range(nlayers):
+        fn(i)
+    gu = llmoe.time_stage_layers(Gs, "gate_up", 5)
+    dn = llmoe.time_stage_layers(Gs, "down", 5)
+    topks = [G.read("topk", (T, K), np.int32) for G in Gs]
+    wb = float(np.mean([gate_up_bytes(L, t) + down_bytes(L, t) for L, t in zip(Ls, topks)]))
+    slots = T * K + (T if shared else 0)
+    t_w = (gu + dn) * 1e-3
+    for G in Gs:
+        G.close()
+    return {"workload": name, "tokens": T, "ms_per_step": dt / steps * 1e3, "tokens_per_s": T * steps / dt,
+            "gate_up_ms": gu, "down_ms": dn, "weight_bytes": wb, "weight_stream_GBps": wb / t_w / 1e9,
+            "weight_stream_frac_peak": wb / t_w / 1e9 / PEAK_HBM_GBS,
+            "int8_TOPS": 2 * slots * 3 * I * H / t_w / 1e12,
+            "int8_mfma_frac_peak": 2 * slots * 3 * I * H / t_w / 1e12 / PEAK_INT8_TOPS}
+
+
 def cpu_baseline(L, x_np, pool, seconds):
     import oracle
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
@@ -246,8 +282,18 @@ def main():
             G.close()
         configs.insert(0, c0)
     if not args.no_stack and not args.only_headline:
+        log("[bench] config 2")
+        configs.append(prefill_config(llmoe, synth, torch, "config 2: 512 tokens, mixed 2/3/4-bit + W8A8 shared, "
+                                      "router x Wr with 1% outlier channels x20, block pool 48", 512, "mixed", True,
+                                      48, None, max(2, args.steps // 10), 2, outliers=0.01))
         log("[bench] config 3")
         configs.append(stack_config(llmoe, synth, torch, max(1, args.steps // 20), max(1, args.warmup // 10)))
+        for bits in (2, 4, 8):
+            for kind in ("uniform", "skewed"):
+                log(f"[bench] config 4: {bits}-bit {kind}")
+                configs.append(prefill_config(llmoe, synth, torch, f"config 4: 4096 tokens, all experts {bits}-bit, "
+                                              f"{kind} routing, no shared expert", 4096, bits, False, 256, kind,
+                                              max(2, args.steps // 40), 1, nlayers=1 if bits == 8 else 2))
 
     p = c1["stage_ms"]
     gu_s = p["gate_up"] * 1e-3
