@@ -88,6 +88,7 @@ __device__ __forceinline__ void unpack_a(const Codes<BITS>& r, const Late& lt, i
         D[4] = b.x; D[5] = b.y; D[6] = b.z; D[7] = b.w;
     } else {
         if constexpr (BITS == 2 || BITS == 3) {
+            // codes 0 .. 2^BITS - 1 select bytes of a table holding c - z for every code (v_perm_b32)
             const u4& u = r.c[tau >> 1];
             const uint32_t p0 = (tau & 1) ? u.z : u.x, p1 = (tau & 1) ? u.w : u.y;
 #pragma unroll
@@ -103,6 +104,13 @@ __device__ __forceinline__ void unpack_a(const Codes<BITS>& r, const Late& lt, i
                     D[s] |= hb & 0x04040404u;
                 }
             }
+            const uint32_t z = (lt.z[tau] >> (8 * (lane & 3))) & 0xFFu;
+            const uint32_t zb = z * 0x01010101u;
+            const uint32_t t_lo = ((0x03020100u | 0x80808080u) - zb) ^ 0x80808080u;   // c - z, c = 0 .. 3
+            const uint32_t t_hi = ((0x07060504u | 0x80808080u) - zb) ^ 0x80808080u;   // c = 4 .. 7
+#pragma unroll
+            for (int s = 0; s < 8; ++s) D[s] = __builtin_amdgcn_perm(t_hi, t_lo, D[s]);
+            return;
         } else {
             const u4& u = r.c[tau];
 #pragma unroll
@@ -163,9 +171,9 @@ __device__ __forceinline__ void prefetch_sb(const uint8_t* p, uint32_t lds_scrat
 // issues all of its activation loads back to back. Returns after the workgroup barrier.
 template <int K>
 __device__ __forceinline__ void stage_chunk(const GemmArgs& a, const Item& it, uint8_t* lds) {
-    constexpr int G = K / GROUP, CH = K / 16, PER = TILED_NTOK * CH / NTHREADS;
+    constexpr int G = K / GROUP, PER = TILED_NTOK * (K / 16) / NTHREADS;
     constexpr int PS = (G * TILED_NTOK + NTHREADS - 1) / NTHREADS;
-    static_assert(PER * NTHREADS == TILED_NTOK * CH, "staging split");
+    static_assert(PER * NTHREADS == TILED_NTOK * (K / 16) && TILED_NTOK == 64, "staging split");
     const int tid = threadIdx.x;
     float* ss = reinterpret_cast<float*>(lds + G * GROUP_B);
     int* sq = reinterpret_cast<int*>(ss + G * TILED_NTOK);
@@ -173,12 +181,22 @@ __device__ __forceinline__ void stage_chunk(const GemmArgs& a, const Item& it, u
     if (tid < TILED_NTOK)
         rowtab[tid] = tid < it.ntok ? (a.slot_token ? a.slot_token[it.slot0 + tid] : it.slot0 + tid) : -1;
     __syncthreads();
+    // thread chunk idx: a wave's 64 lanes cover 8 tokens x the 8 16-byte chunks of one group, i.e. one
+    // contiguous, bank-conflict-free KiB of LDS; consecutive lanes read 128 contiguous bytes of a row
+    auto chunk = [&](int idx, int& n, int& g, int& c16) {
+        const int b = idx >> 6, l = idx & 63;
+        g = b >> 3;
+        n = ((b & 7) << 3) + (l >> 3);
+        c16 = l & 7;
+    };
     u4 v[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const int idx = tid + NTHREADS * i, n = idx / CH, c = idx % CH;
+        int n, g, c16;
+        chunk(tid + NTHREADS * i, n, g, c16);
         const int row = rowtab[n];
-        v[i] = row >= 0 ? *reinterpret_cast<const u4*>(a.xq + size_t(row) * K + 16 * c) : u4{0u, 0u, 0u, 0u};
+        v[i] = row >= 0 ? *reinterpret_cast<const u4*>(a.xq + size_t(row) * K + g * GROUP + 16 * c16)
+                        : u4{0u, 0u, 0u, 0u};
     }
     float sv[PS];
     int qv[PS];
@@ -191,7 +209,8 @@ __device__ __forceinline__ void stage_chunk(const GemmArgs& a, const Item& it, u
     }
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const int idx = tid + NTHREADS * i, n = idx / CH, c = idx % CH, g = c >> 3, c16 = c & 7;
+        int n, g, c16;
+        chunk(tid + NTHREADS * i, n, g, c16);
         *reinterpret_cast<u4*>(lds + g * GROUP_B + n * GROUP + ((c16 ^ (n & 7)) << 4)) = v[i];
     }
 #pragma unroll
