@@ -26,7 +26,7 @@ typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 
 constexpr int NW = TILED_WAVES;                 // waves per workgroup
 constexpr int NTHREADS = NW * 64;
-constexpr int NTILE = TILED_NTOK / 16;          // 16-token tiles per chunk
+constexpr int MAX_TILE = TILED_NTOK / 16;       // 16-token tiles per chunk
 // LDS: activations [group][token][128 B] (16-byte chunk c of token n at ((c ^ (n & 7)) * 16)), then fp32 scales
 // and negated int32 sums [group][token], then the chunk's row table [token]
 constexpr int GROUP_B = TILED_NTOK * GROUP;
@@ -239,7 +239,7 @@ __device__ __forceinline__ void prefetch_step(const GemmArgs& a, const Item& it,
         prefetch_sb<BITS>(mat + (size_t((rb * NW + wave) * S + s) * NSB + sb) * sb_bytes(BITS), scratch, lane);
 }
 
-template <int BITS, int MODE>
+template <int BITS, int MODE, int NTILE>
 __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it, const uint8_t* lds, int rb,
                                                int rb_end, uint32_t scratch) {
     constexpr bool DOWN = MODE == GEMM_DOWN;
@@ -385,7 +385,7 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
     }
 }
 
-template <int BITS, int MODE>
+template <int BITS, int MODE, int NTILE>
 __device__ __forceinline__ void tiled_body(const GemmArgs& a, const Item& it, uint8_t* lds) {
     constexpr int K = MODE == GEMM_DOWN ? 512 : 2048;
     constexpr int NSB = K / SB_K;
@@ -398,7 +398,7 @@ __device__ __forceinline__ void tiled_body(const GemmArgs& a, const Item& it, ui
     for (int t = 0; t < PF_STEPS; ++t)
         if (rb0 + t / NSB < rb0 + nrb) prefetch_step<BITS, MODE>(a, it, rb0 + t / NSB, t % NSB, scratch);
     stage_chunk<K>(a, it, lds);
-    for (int rb = rb0; rb < rb0 + nrb; ++rb) tiled_rowblock<BITS, MODE>(a, it, lds, rb, rb0 + nrb, scratch);
+    for (int rb = rb0; rb < rb0 + nrb; ++rb) tiled_rowblock<BITS, MODE, NTILE>(a, it, lds, rb, rb0 + nrb, scratch);
 }
 
 template <int MODE>
@@ -408,13 +408,27 @@ __global__ void __launch_bounds__(NTHREADS) tiled_gemm(GemmArgs a) {
     for (int u = blockIdx.x; u < n; u += gridDim.x) {
         const Item it = a.items[u];
         const int bits = a.bits[it.expert];
+        // token tiles actually present (a chunk has <= 64 slots; absent tiles are not computed)
+        const int nt = (it.ntok + 15) >> 4;
 #ifdef TILED_ONLY
-        tiled_body<TILED_ONLY, MODE>(a, it, lds);
+        tiled_body<TILED_ONLY, MODE, 4>(a, it, lds);
 #else
-        if (bits == 2) tiled_body<2, MODE>(a, it, lds);
-        else if (bits == 3) tiled_body<3, MODE>(a, it, lds);
-        else if (bits == 4) tiled_body<4, MODE>(a, it, lds);
-        else tiled_body<8, MODE>(a, it, lds);
+        if (nt > 3) {
+            if (bits == 2) tiled_body<2, MODE, 4>(a, it, lds);
+            else if (bits == 3) tiled_body<3, MODE, 4>(a, it, lds);
+            else if (bits == 4) tiled_body<4, MODE, 4>(a, it, lds);
+            else tiled_body<8, MODE, 4>(a, it, lds);
+        } else if (nt == 3) {
+            if (bits == 2) tiled_body<2, MODE, 3>(a, it, lds);
+            else if (bits == 3) tiled_body<3, MODE, 3>(a, it, lds);
+            else if (bits == 4) tiled_body<4, MODE, 3>(a, it, lds);
+            else tiled_body<8, MODE, 3>(a, it, lds);
+        } else {
+            if (bits == 2) tiled_body<2, MODE, 2>(a, it, lds);
+            else if (bits == 3) tiled_body<3, MODE, 2>(a, it, lds);
+            else if (bits == 4) tiled_body<4, MODE, 2>(a, it, lds);
+            else tiled_body<8, MODE, 2>(a, it, lds);
+        }
 #endif
         __syncthreads();   // the next unit re-stages the activations
     }
