@@ -253,6 +253,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-headline", action="store_true", help="config 1 only (profiling runs)")
+    ap.add_argument("--only-stack", action="store_true", help="config 3 only (profiling runs of the tiled GEMM)")
     ap.add_argument("--copy-calibration", action="store_true", help="run 512 MiB device copies first (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -269,6 +270,9 @@ def main():
     if args.copy_calibration:
         copy_calibration(torch)
 
+    if args.only_stack:
+        print(json.dumps(stack_config(llmoe, synth, torch, max(1, args.steps // 20), max(1, args.warmup // 10))))
+        return
     log("[bench] config 1 (headline)")
     c1, (L1, G1s, x1, _, _) = one_layer_config(llmoe, synth, torch, "config 1: 32 tokens, mixed 2/3/4-bit + W8A8 "
                                               "shared, uniform-random routing (no pool)", 1, 32, "mixed", True, 256,

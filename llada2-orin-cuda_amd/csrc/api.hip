@@ -122,7 +122,7 @@ int check_layer(const llmoe_layer* L) {
 int nblocks(const llmoe_layer* L, int T) { return (T + L->d.block - 1) / L->d.block; }
 
 // streamed work items hold 16 slots; the item capacity for T tokens (experts with more than TILED_MIN slots take
-// tiled units instead when T > TILED_MIN)
+// tiled units instead when the routing spans several blocks)
 void choose_items(llmoe_layer* L, int T) {
     const auto& d = L->d;
     const long eff = std::min<long>(d.n_experts, long(nblocks(L, T)) * std::min(d.pool, d.n_experts));
@@ -130,7 +130,7 @@ void choose_items(llmoe_layer* L, int T) {
     const long routed = eff + (long(T) * d.top_k + L->ntok - 1) / L->ntok;
     const long shared = d.has_shared ? (T + L->ntok - 1) / L->ntok : 0;
     L->max_items = int(routed + shared);
-    L->tiled = T > TILED_MIN;
+    L->tiled = T > d.block && T > TILED_MIN;   // the single-block decode routing emits streamed units only
 }
 
 int check_T(const llmoe_layer* L, int T) {

@@ -39,7 +39,7 @@ constexpr int MAX_UNITS_PER_ITEM = 16;   // gemm_row_blocks(false, 8)
 // and its TILED_WAVES waves stream tiled_spw strips each per row block. An expert takes tiled units when it has
 // more than TILED_MIN slots, otherwise streamed units of 16 slots.
 constexpr int TILED_NTOK = 64;
-constexpr int TILED_MIN = 40;
+constexpr int TILED_MIN = 16;
 constexpr int TILED_WAVES = 8;
 __host__ __device__ constexpr int tiled_spw(int bits) { return bits == 8 ? 1 : 2; }
 __host__ __device__ constexpr int tiled_row_blocks(bool down, int bits) {

@@ -160,75 +160,6 @@ __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int o) {
     return (uint64_t(hi) << 32) | lo;
 }
 
-// exclusive prefix sum over the NT threads of a block (Hillis-Steele in LDS); *total = the full sum
-template <int NT>
-__device__ int block_excl_scan(int v, int* buf, int* total) {
-    const int i = threadIdx.x;
-    buf[i] = v;
-    __syncthreads();
-    for (int o = 1; o < NT; o <<= 1) {
-        const int add = i >= o ? buf[i - o] : 0;
-        __syncthreads();
-        buf[i] += add;
-        __syncthreads();
-    }
-    const int incl = buf[i];
-    *total = buf[NT - 1];
-    __syncthreads();
-    return incl - v;
-}
-
-// Work-unit offsets ordered heaviest first: the shared expert's units, then routed experts by code width (8, 4,
-// 3, 2 bits), expert ascending inside a width -- long workgroups start first. Wave 0, 4 experts per lane.
-// nu_gu / nu_dn: units per expert (LDS); cls: width class 0..3 per expert (LDS); sh_gu / sh_dn: shared units.
-// Out (LDS): base_gu / base_dn per expert, tot[0] / tot[1] = total units. All threads must call it.
-__device__ void unit_offsets(const int* nu_gu, const int* nu_dn, const int* cls, int E, int sh_gu, int sh_dn,
-                             int* base_gu, int* base_dn, int* tot) {
-    if (threadIdx.x < 64) {
-        const int l = threadIdx.x;
-        int bg = sh_gu, bd = sh_dn;
-        for (int c = 0; c < 4; ++c) {
-            int vg[4], vd[4], sg = 0, sd = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int e = 4 * l + j;
-                const bool in = e < E && cls[e] == c;
-                vg[j] = in ? nu_gu[e] : 0;
-                vd[j] = in ? nu_dn[e] : 0;
-                sg += vg[j];
-                sd += vd[j];
-            }
-            int ig = sg, id = sd;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int tg = __shfl_up(ig, o), td = __shfl_up(id, o);
-                if (l >= o) {
-                    ig += tg;
-                    id += td;
-                }
-            }
-            int rg = bg + ig - sg, rd = bd + id - sd;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int e = 4 * l + j;
-                if (e < E && cls[e] == c) {
-                    base_gu[e] = rg;
-                    base_dn[e] = rd;
-                }
-                rg += vg[j];
-                rd += vd[j];
-            }
-            bg += __shfl(ig, 63);
-            bd += __shfl(id, 63);
-        }
-        if (l == 0) {
-            tot[0] = bg;
-            tot[1] = bd;
-        }
-    }
-    __syncthreads();
-}
-
 __device__ __forceinline__ int width_class(int bits) { return bits == 8 ? 0 : bits == 4 ? 1 : bits == 3 ? 2 : 3; }
 
 // the units of expert e: items of <= ntok of its c slots starting at slot st, each split into row blocks
@@ -697,56 +628,108 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
                                                    Item* __restrict__ units_gu, Item* __restrict__ units_dn,
                                                    Item* __restrict__ tunits_gu, Item* __restrict__ tunits_dn,
                                                    int* __restrict__ n_units) {
-    __shared__ int buf[256];
-    __shared__ int nu_gu[MAXE], nu_dn[MAXE], ub_gu[MAXE], ub_dn[MAXE], wcls[MAXE], utot[2];
-    __shared__ int tu_gu[MAXE], tu_dn[MAXE], tb_gu[MAXE], tb_dn[MAXE], ttot[2];
-    const int e = threadIdx.x, nb = (T + block - 1) / block;
+    constexpr int NBR = 64;                    // token masks of the first NBR blocks stay in registers
+    __shared__ int wt_i[4], wt_c[4];
+    __shared__ uint64_t wt[4][4];
+    __shared__ uint64_t tot[4];
+    const int e = threadIdx.x, nb = (T + block - 1) / block, lane = e & 63, w = e >> 6;
+    uint32_t mv[NBR];
+#pragma unroll
+    for (int j = 0; j < NBR; ++j) mv[j] = e < E && j < nb ? mask[size_t(j) * E + e] : 0u;   // one batch of loads
     int c = 0;
+#pragma unroll
+    for (int j = 0; j < NBR; ++j) c += __popc(mv[j]);
     if (e < E)
-        for (int b = 0; b < nb; ++b) c += __popc(mask[size_t(b) * E + e]);
-    int tot_slots;
-    const int st = block_excl_scan<256>(c, buf, &tot_slots);
-    const bool big = tiled && c > TILED_MIN;
+        for (int b = NBR; b < nb; ++b) c += __popc(mask[size_t(b) * E + e]);
+    const bool big = e < E && tiled && c > TILED_MIN;
     const bool sbig = has_shared && tiled && T > TILED_MIN;
     const int nsch = sbig ? tiled_chunks(T) : 0;
-    // row-block ranges per chunk: enough tiled units to fill the GPU (split a chunk's rows when chunks are few)
-    int all_chunks;
-    block_excl_scan<256>(e < E && big ? tiled_chunks(c) : 0, buf, &all_chunks);
-    all_chunks += nsch;
-    const int split = all_chunks >= 384 ? 1 : all_chunks >= 192 ? 2 : 4;
-    if (e < E) {
-        const int bw = bits[e];
-        const int nit = big ? 0 : (c + ntok - 1) / ntok, nch = big ? tiled_chunks(c) : 0;
-        nu_gu[e] = nit * gemm_row_blocks(false, bw);
-        nu_dn[e] = nit * gemm_row_blocks(true, bw);
-        tu_gu[e] = nch * split;
-        tu_dn[e] = nch * split;
-        wcls[e] = width_class(bw);
+    const int bw = e < E ? bits[e] : 2, cls = width_class(bw);
+    const int nit = e < E && !big ? (c + ntok - 1) / ntok : 0, nch = big ? tiled_chunks(c) : 0;
+    // one pass of inclusive scans over the experts: slots, tiled chunks, and per width class (16-bit fields) the
+    // streamed and tiled units of both lists; the chunk total decides the row split of the tiled units first
+    int incl = c, inch = nch;
+    uint64_t s0 = uint64_t(nit * gemm_row_blocks(false, bw)) << (16 * cls);
+    uint64_t s1 = uint64_t(nit * gemm_row_blocks(true, bw)) << (16 * cls);
+    uint64_t t0 = uint64_t(nch) << (16 * cls);
+    const uint64_t own0 = s0, own1 = s1, ownt = t0;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int a1 = __shfl_up(incl, o), a2 = __shfl_up(inch, o);
+        const uint64_t b0 = __shfl_up(s0, o), b1 = __shfl_up(s1, o), b2 = __shfl_up(t0, o);
+        if (lane >= o) {
+            incl += a1;
+            inch += a2;
+            s0 += b0;
+            s1 += b1;
+            t0 += b2;
+        }
+    }
+    if (lane == 63) {
+        wt_i[w] = incl;
+        wt_c[w] = inch;
+        wt[w][0] = s0;
+        wt[w][1] = s1;
+        wt[w][2] = t0;
     }
     __syncthreads();
+    for (int i = 0; i < w; ++i) {
+        incl += wt_i[i];
+        inch += wt_c[i];
+        s0 += wt[i][0];
+        s1 += wt[i][1];
+        t0 += wt[i][2];
+    }
+    if (e == 255) {
+        tot[0] = s0;
+        tot[1] = s1;
+        tot[2] = t0;
+        wt_i[0] = inch;            // all routed chunks (read after the barrier below)
+    }
+    __syncthreads();
+    const int all_chunks = wt_i[0] + nsch;
+    // row-block ranges per chunk: enough tiled units to fill the GPU (split a chunk's rows when chunks are few)
+    const int split = all_chunks >= 384 ? 1 : all_chunks >= 192 ? 2 : 4;
     const int sbits = has_shared ? bits[E] : 8;
     const int ns = has_shared && !sbig ? (T + ntok - 1) / ntok : 0;
-    unit_offsets(nu_gu, nu_dn, wcls, E, ns * gemm_row_blocks(false, sbits), ns * gemm_row_blocks(true, sbits), ub_gu,
-                 ub_dn, utot);
-    unit_offsets(tu_gu, tu_dn, wcls, E, nsch * split, nsch * split, tb_gu, tb_dn, ttot);
+    // offsets: the shared expert's units first, then width classes 0 .. 3 (8, 4, 3, 2 bits), expert ascending
+    int bg = ns * gemm_row_blocks(false, sbits), bd = ns * gemm_row_blocks(true, sbits), bt = nsch * split;
+    int og = 0, od = 0, ot = 0;
+    for (int k = 0; k < 4; ++k) {
+        if (k == cls) {
+            og = bg + int(((s0 - own0) >> (16 * k)) & 0xFFFFu);
+            od = bd + int(((s1 - own1) >> (16 * k)) & 0xFFFFu);
+            ot = bt + split * int(((t0 - ownt) >> (16 * k)) & 0xFFFFu);
+        }
+        bg += int((tot[0] >> (16 * k)) & 0xFFFFu);
+        bd += int((tot[1] >> (16 * k)) & 0xFFFFu);
+        bt += split * int((tot[2] >> (16 * k)) & 0xFFFFu);
+    }
+    const int st = incl - c;
     if (e < E) {
         count[e] = c;
         start[e] = st;
         int run = st;
-        for (int b = 0; b < nb; ++b) {
+#pragma unroll
+        for (int j = 0; j < NBR; ++j)
+            if (j < nb) {
+                bpre[size_t(j) * E + e] = run;
+                run += __popc(mv[j]);
+            }
+        for (int b = NBR; b < nb; ++b) {
             bpre[size_t(b) * E + e] = run;
             run += __popc(mask[size_t(b) * E + e]);
         }
-        if (big) emit_tiled_units(e, c, st, bits[e], split, tb_gu[e], tb_dn[e], tunits_gu, tunits_dn);
-        else emit_units(e, c, st, ntok, bits[e], ub_gu[e], ub_dn[e], units_gu, units_dn);
+        if (big) emit_tiled_units(e, c, st, bw, split, ot, ot, tunits_gu, tunits_dn);
+        else emit_units(e, c, st, ntok, bw, og, od, units_gu, units_dn);
     }
     if (ns) emit_shared_units(E, T, K, ntok, sbits, units_gu, units_dn);
     if (sbig) emit_shared_tiled_units(E, T, K, sbits, split, tunits_gu, tunits_dn);
-    if (threadIdx.x == 0) {
-        n_units[0] = utot[0];
-        n_units[1] = utot[1];
-        n_units[2] = ttot[0];
-        n_units[3] = ttot[1];
+    if (e == 0) {
+        n_units[0] = bg;
+        n_units[1] = bd;
+        n_units[2] = bt;
+        n_units[3] = bt;
     }
 }
 
