@@ -24,6 +24,8 @@
  *   llmoe_dispatch        the host counting sort of engine/tests/test_moe_i8.cu:73-98 (externally routed)
  *   llmoe_experts         gemm<..,0> -> fwht512_q8 -> gemm<..,1> -> combine (engine/engine.cu:461-478,
  *                         engine/moe_i8.cu:408-515)
+ *   llmoe_experts_norm    llmoe_experts + ops::moe_combine_norm (engine/ops.cu:507-549): un-rotation, residual,
+ *                         next-layer RMSNorm / rotation / A8
  *   llmoe_layer_forward   the MoE half of Engine::layer_step / Engine::prefill (engine/engine.cu:445-479,
  *                         :616-649), without the norm/rotation before it and the un-rotation after it
  */
@@ -88,6 +90,18 @@ int llmoe_dispatch(llmoe_layer* layer, const int32_t* topk, const float* topw, i
  *   out[t] = sum_k w[t,k] expert_k(x_t) (+ shared(x_t)), summed in rank order, shared last. */
 int llmoe_experts(llmoe_layer* layer, const int8_t* xq, const float* xs, const int32_t* xsum, int T, float* out,
                   llmoe_stream stream);
+
+/* llmoe_experts with the combine's consumer fused in (engine/ops.cu:507-549, moe_combine_norm): the combined
+ * expert output, still in the rotated basis, is un-rotated and added to the residual stream, and the next layer's
+ * input norm is applied:
+ *   h[t] += (FWHT2048(sum_k Y_k) * signs) / sqrt(2048)                     (Q^T = H diag(signs) / sqrt(2048))
+ *   (q_next, s_next, sum_next) = A8(FWHT2048((h[t] / rms(h[t], eps)) * signs) / sqrt(2048))
+ * signs fp32 [2048] of +-1 (the residual rotation), h fp32 [T, 2048] in/out, q_next int8 [T, 2048], s_next fp32
+ * [T, 16], sum_next int32 [T, 16] (the llmoe_quantize_a8 layout; RMSNorm gamma is folded into the next
+ * layer's weights). hidden must be 2048. */
+int llmoe_experts_norm(llmoe_layer* layer, const int8_t* xq, const float* xs, const int32_t* xsum, int T,
+                       const float* signs, float eps, float* h, int8_t* q_next, float* s_next, int32_t* sum_next,
+                       llmoe_stream stream);
 
 /* Whole layer: A8(x) -> route (x Wr, or the given logits) -> experts -> out. x fp32 [T, H]. */
 int llmoe_layer_forward(llmoe_layer* layer, const float* x, const float* logits, int T, float* out,

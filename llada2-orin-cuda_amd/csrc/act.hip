@@ -141,6 +141,135 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
     }
 }
 
+// FWHT-2048 of the workgroup's 2048 values, stages h = 1 .. 1024 ascending. On entry thread i holds values
+// 8i .. 8i+7 (layout A); bits 0-2 in registers, bits 3-8 by lane shuffles (xor 1 .. 32), then an LDS transpose
+// gives thread i the values i + 256 j (layout B) for bits 9-10. On exit x holds layout B.
+__device__ __forceinline__ void fwht2048_ab(float (&x)[8], float* v) {
+    const int i = threadIdx.x, lane = i & 63;
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (!(j & h)) {
+                const float a = x[j], b = x[j + h];
+                x[j] = a + b;
+                x[j + h] = a - b;
+            }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const bool hi = lane & o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float y = __shfl_xor(x[j], o);
+            x[j] = hi ? y - x[j] : x[j] + y;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[8 * i + j] = x[j];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = v[i + 256 * j];
+#pragma unroll
+    for (int h = 2; h < 8; h <<= 1)                       // index bits 9, 10 (j bits 1, 2)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (!(j & h)) {
+                const float a = x[j], b = x[j + h];
+                x[j] = a + b;
+                x[j + h] = a - b;
+            }
+    __syncthreads();                                      // v is reused by the caller
+}
+
+// Combine + un-rotation + residual + the next layer's RMSNorm, rotation and A8 (engine/ops.cu:507-549), H = 2048.
+// grid T, 256 threads:
+//   x = sum_k Y[tok_slots[t, k]] (k ascending); h[t] += (FWHT(x) signs) / sqrt(2048);
+//   r = 1 / sqrt(sum h[t]^2 / 2048 + eps); y = FWHT((h[t] r) signs) / sqrt(2048); (q, s, sum) = A8(y)
+// Sum of squares: thread i adds h[i + 256 j]^2 for j ascending, a 64-lane xor butterfly, then the 4 wave sums in
+// order -- the order the CPU checker uses.
+constexpr float INV_SQRT_2048 = 0.02209708691207961f;
+__global__ void __launch_bounds__(256) combine_norm_kernel(const float* __restrict__ Y, const int* __restrict__ tok_slots,
+                                                           int kk, int K1, const float* __restrict__ signs, float eps,
+                                                           float* __restrict__ h, int8_t* __restrict__ q,
+                                                           float* __restrict__ s, int* __restrict__ sum) {
+    __shared__ __align__(16) float v[2048];
+    __shared__ float red[4];
+    const int t = blockIdx.x, i = threadIdx.x, lane = i & 63;
+    int sl[MAX_KK];
+#pragma unroll
+    for (int k = 0; k < MAX_KK; ++k) sl[k] = k < kk ? tok_slots[t * K1 + k] : 0;
+    float4 ya[MAX_KK], yb[MAX_KK];
+#pragma unroll
+    for (int k = 0; k < MAX_KK; ++k)
+        if (k < kk) {
+            const float4* yp = reinterpret_cast<const float4*>(Y + size_t(sl[k]) * 2048 + 8 * i);
+            ya[k] = yp[0];
+            yb[k] = yp[1];
+        }
+    float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < MAX_KK; ++k)
+        if (k < kk) {
+            x[0] = x[0] + ya[k].x; x[1] = x[1] + ya[k].y; x[2] = x[2] + ya[k].z; x[3] = x[3] + ya[k].w;
+            x[4] = x[4] + yb[k].x; x[5] = x[5] + yb[k].y; x[6] = x[6] + yb[k].z; x[7] = x[7] + yb[k].w;
+        }
+    fwht2048_ab(x, v);
+    float* hr = h + size_t(t) * 2048;
+    float sg[8];
+    float p = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int c = i + 256 * j;
+        sg[j] = signs[c];
+        x[j] = hr[c] + (x[j] * sg[j]) * INV_SQRT_2048;
+        hr[c] = x[j];
+        p = p + x[j] * x[j];
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) p = p + __shfl_xor(p, o);
+    if (lane == 0) red[i >> 6] = p;
+    __syncthreads();
+    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
+    const float r = 1.0f / sqrtf(tot / 2048.0f + eps);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[i + 256 * j] = (x[j] * r) * sg[j];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = v[8 * i + j];
+    __syncthreads();
+    fwht2048_ab(x, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[i + 256 * j] = x[j] * INV_SQRT_2048;
+    __syncthreads();
+    // A8 per 128-group: wave w takes columns 512 w .. 512 w + 511, 16 lanes per group (as quant_a8_kernel)
+    const float* vv = v + 512 * (i >> 6) + 8 * lane;
+    float m = 0.0f;
+    float val[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        val[j] = vv[j];
+        m = fmaxf(m, fabsf(val[j]));
+    }
+    m = group16_max(m);
+    const float sc = fmaxf(m / 127.0f, 1e-30f);
+    int totq = 0;
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int qq = clamp127(__builtin_rintf(val[j] / sc));
+        totq += qq;
+        if (j < 4) w0 |= uint32_t(qq & 0xFF) << (8 * j);
+        else w1 |= uint32_t(qq & 0xFF) << (8 * (j - 4));
+    }
+    *reinterpret_cast<uint2*>(q + size_t(t) * 2048 + 512 * (i >> 6) + 8 * lane) = make_uint2(w0, w1);
+    totq = group16_sum(totq);
+    if ((lane & 15) == 0) {
+        const size_t gi = size_t(t) * 16 + 4 * (i >> 6) + (lane >> 4);
+        s[gi] = sc;
+        sum[gi] = totq;
+    }
+}
+
 }  // namespace
 
 hipError_t launch_quant_a8(const float* x, int rows, int cols, int8_t* q, float* s, int* sum, hipStream_t st) {
@@ -153,6 +282,14 @@ hipError_t launch_quant_a8(const float* x, int rows, int cols, int8_t* q, float*
 hipError_t launch_fwht_a8(const uint16_t* Z, int nslots, int8_t* q, float* s, int* sum, hipStream_t st) {
     if (nslots <= 0) return hipSuccess;
     fwht_a8_kernel<<<(nslots + 3) / 4, 256, 0, st>>>(Z, nslots, q, s, sum);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine_norm(const float* Y, const int* tok_slots, int T, int kk, int K1, const float* signs,
+                               float eps, float* h, int8_t* q, float* s, int* sum, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    if (kk > MAX_KK) return hipErrorInvalidValue;
+    combine_norm_kernel<<<T, 256, 0, st>>>(Y, tok_slots, kk, K1, signs, eps, h, q, s, sum);
     return hipGetLastError();
 }
 

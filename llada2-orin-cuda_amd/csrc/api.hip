@@ -374,13 +374,22 @@ int llmoe_dispatch(llmoe_layer* L, const int32_t* topk, const float* topw, int T
     return plan_and_place(L, L->topk, L->topw, T, st);
 }
 
-int llmoe_experts(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_t* xsum, int T, float* out,
-                  llmoe_stream stream) {
-    if (int rc = check_layer(L)) return rc;
-    if (!xq || !xs || !xsum || !out) return fail(LLMOE_EINVAL, "null argument");
+}  // extern "C"
+
+namespace {
+struct NormOut {            // the combine's fused epilogue (llmoe_experts_norm); h == nullptr: plain combine
+    const float* signs;
+    float eps;
+    float* h;
+    int8_t* q;
+    float* s;
+    int32_t* sum;
+};
+
+int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_t* xsum, int T, float* out,
+                 const NormOut& no, hipStream_t st) {
     if (T != L->routed_T) return fail(LLMOE_ESTATE, "no routing for T = %d (route or dispatch first)", T);
     const auto& d = L->d;
-    const hipStream_t st = static_cast<hipStream_t>(stream);
     const int H = d.hidden, I = d.inter, K = d.top_k;
     const int S = T * K + (d.has_shared ? T : 0);
     GemmArgs g{};
@@ -422,9 +431,35 @@ int llmoe_experts(llmoe_layer* L, const int8_t* xq, const float* xs, const int32
     HIPCHECK(launch_gemm(GEMM_DOWN, g, tg, L->tiled, st));
     L->mark(LLMOE_STAGE_DOWN, true, st);
     L->mark(LLMOE_STAGE_COMBINE, false, st);
-    HIPCHECK(launch_combine(L->Y, L->tok_slots, T, H, K + (d.has_shared ? 1 : 0), K + 1, out, st));
+    if (no.h)
+        HIPCHECK(launch_combine_norm(L->Y, L->tok_slots, T, K + (d.has_shared ? 1 : 0), K + 1, no.signs, no.eps, no.h,
+                                     no.q, no.s, no.sum, st));
+    else
+        HIPCHECK(launch_combine(L->Y, L->tok_slots, T, H, K + (d.has_shared ? 1 : 0), K + 1, out, st));
     L->mark(LLMOE_STAGE_COMBINE, true, st);
     return LLMOE_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int llmoe_experts(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_t* xsum, int T, float* out,
+                  llmoe_stream stream) {
+    if (int rc = check_layer(L)) return rc;
+    if (!xq || !xs || !xsum || !out) return fail(LLMOE_EINVAL, "null argument");
+    return experts_impl(L, xq, xs, xsum, T, out, NormOut{}, static_cast<hipStream_t>(stream));
+}
+
+int llmoe_experts_norm(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_t* xsum, int T,
+                       const float* signs, float eps, float* h, int8_t* q_next, float* s_next, int32_t* sum_next,
+                       llmoe_stream stream) {
+    if (int rc = check_layer(L)) return rc;
+    if (!xq || !xs || !xsum || !signs || !h || !q_next || !s_next || !sum_next)
+        return fail(LLMOE_EINVAL, "null argument");
+    if (L->d.hidden != 2048) return fail(LLMOE_EINVAL, "the rotation is FWHT-2048: hidden must be 2048");
+    if (L->d.top_k + (L->d.has_shared ? 1 : 0) > 9) return fail(LLMOE_EINVAL, "at most 9 slots per token");
+    return experts_impl(L, xq, xs, xsum, T, nullptr, NormOut{signs, eps, h, q_next, s_next, sum_next},
+                        static_cast<hipStream_t>(stream));
 }
 
 int llmoe_layer_forward(llmoe_layer* L, const float* x, const float* logits, int T, float* out, llmoe_stream stream) {

@@ -149,6 +149,9 @@ hipError_t launch_tiled_gemm(int mode, const GemmArgs& a, hipStream_t st);
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, int R, int K, int bits, int gate_up, hipStream_t st);
 hipError_t launch_quant_a8(const float* x, int rows, int cols, int8_t* q, float* s, int* sum, hipStream_t st);
 hipError_t launch_fwht_a8(const uint16_t* Z, int nslots, int8_t* q, float* s, int* sum, hipStream_t st);
+// combine + FWHT-2048 un-rotation + residual into h + next-layer RMSNorm / rotation / A8 (H = 2048)
+hipError_t launch_combine_norm(const float* Y, const int* tok_slots, int T, int kk, int K1, const float* signs,
+                               float eps, float* h, int8_t* q, float* s, int* sum, hipStream_t st);
 hipError_t launch_combine(const float* Y, const int* tok_slots, int T, int H, int kk, int K1, float* out,
                           hipStream_t st);
 // router logits partials; with q != nullptr also the A8 of x (q, qs, qsum as launch_quant_a8), H = 2048

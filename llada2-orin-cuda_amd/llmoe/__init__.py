@@ -61,7 +61,7 @@ class Buffers(ctypes.Structure):
 
 EXPORTS = [
     "llmoe_layer_create", "llmoe_layer_destroy", "llmoe_quantize_a8", "llmoe_route", "llmoe_dispatch",
-    "llmoe_experts", "llmoe_layer_forward", "llmoe_layer_buffers", "llmoe_layer_weight_bytes",
+    "llmoe_experts", "llmoe_experts_norm", "llmoe_layer_forward", "llmoe_layer_buffers", "llmoe_layer_weight_bytes",
     "llmoe_group_products", "llmoe_layer_set_profiling", "llmoe_layer_stage_ms", "llmoe_layer_time_stage", "llmoe_layers_time_stage",
     "llmoe_last_error",
 ]
@@ -89,6 +89,7 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.llmoe_route.argtypes = [vp, vp, vp, i, vp]
     lib.llmoe_dispatch.argtypes = [vp, vp, vp, i, vp]
     lib.llmoe_experts.argtypes = [vp, vp, vp, vp, i, vp, vp]
+    lib.llmoe_experts_norm.argtypes = [vp, vp, vp, vp, i, vp, f, vp, vp, vp, vp, vp]
     lib.llmoe_layer_forward.argtypes = [vp, vp, vp, i, vp, vp]
     lib.llmoe_layer_buffers.argtypes = [vp, ctypes.POINTER(Buffers)]
     lib.llmoe_layer_weight_bytes.argtypes = [vp, ctypes.POINTER(sz)]
@@ -185,6 +186,18 @@ class Layer:
             out = torch.empty((T, self.desc.hidden), dtype=torch.float32, device=xq.device)
         _check(self.lib.llmoe_experts(self.handle, _ptr(xq), _ptr(xs), _ptr(xsum), T, _ptr(out), _stream(stream)))
         return out
+
+    def experts_norm(self, xq, xs, xsum, signs, eps, h, stream=None):
+        """Experts, then un-rotation + residual into h (in place) + the next layer's RMSNorm / rotation / A8.
+        Returns (q_next, s_next, sum_next)."""
+        import torch
+        T = xq.shape[0]
+        q = torch.empty((T, 2048), dtype=torch.int8, device=xq.device)
+        s = torch.empty((T, 16), dtype=torch.float32, device=xq.device)
+        sm = torch.empty((T, 16), dtype=torch.int32, device=xq.device)
+        _check(self.lib.llmoe_experts_norm(self.handle, _ptr(xq), _ptr(xs), _ptr(xsum), T, _ptr(signs), float(eps),
+                                           _ptr(h), _ptr(q), _ptr(s), _ptr(sm), _stream(stream)))
+        return q, s, sm
 
     def group_products(self, expert: int, which: int, xq, xsum, stream=None):
         import torch

@@ -598,3 +598,64 @@ int orc_reference_f64(const orc_layer* L, const float* x, int T, const int32_t* 
     free(xd);
     return err ? -1 : 0;
 }
+
+/* ---- combine + un-rotation + residual + next-layer norm / rotation / A8 (engine/ops.cu:507-549) ---------------
+ * Unnormalised Sylvester FWHT of n values, stages h = 1, 2, ..., n/2 ascending (engine/ops.cu:458-474 and the
+ * bits 8-10 stages of :477-505 run in the same ascending order). */
+static void fwht_n(float* v, int n) {
+    for (int h = 1; h < n; h <<= 1)
+        for (int j = 0; j < n; ++j)
+            if (!(j & h)) {
+                const float a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
+}
+
+#define INV_SQRT_2048 0.02209708691207961f
+
+/* Per token t (H = 2048):
+ *   x = sum_k Y[tok_slots[t, k]] (k = 0 .. nk-1 ascending, from 0)                       engine/ops.cu:515-520
+ *   h[t] = h[t] + (FWHT(x) * signs) * 2048^-1/2                                          :521-535 (un-rotation)
+ *   r = 1 / sqrt(sum(h[t]^2) / 2048 + eps); y = FWHT((h[t] * r) * signs) * 2048^-1/2     :74-114 (norm_rot_body)
+ *   (q, s, sum) = A8(y)                                                                   :40-66
+ * The sum of squares follows the GPU's tree: thread i (0 .. 255) adds h[i + 256 j]^2 for j = 0 .. 7 in order,
+ * a 64-lane xor butterfly (1, 2, .., 32) sums each wave, and the 4 wave sums are added in order. */
+void orc_combine_norm(const float* Y, const int32_t* tok_slots, int T, int nk, int K1, const float* signs, float eps,
+                      float* h, int8_t* q, float* s, int32_t* sum) {
+    enum { H = 2048 };
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < T; ++t) {
+        float x[H], part[256];
+        for (int c = 0; c < H; ++c) x[c] = 0.0f;
+        for (int k = 0; k < nk; ++k) {
+            const float* y = Y + (size_t)tok_slots[(size_t)t * K1 + k] * H;
+            for (int c = 0; c < H; ++c) x[c] = x[c] + y[c];
+        }
+        fwht_n(x, H);
+        float* hr = h + (size_t)t * H;
+        for (int c = 0; c < H; ++c) hr[c] = hr[c] + (x[c] * signs[c]) * INV_SQRT_2048;
+        for (int i = 0; i < 256; ++i) {
+            float p = 0.0f;
+            for (int j = 0; j < 8; ++j) p = p + hr[i + 256 * j] * hr[i + 256 * j];
+            part[i] = p;
+        }
+        float tot = 0.0f;
+        for (int w = 0; w < 4; ++w) {
+            float a[64], b[64];
+            for (int l = 0; l < 64; ++l) a[l] = part[64 * w + l];
+            for (int o = 1; o < 64; o <<= 1) {
+                for (int l = 0; l < 64; ++l) b[l] = a[l] + a[l ^ o];
+                for (int l = 0; l < 64; ++l) a[l] = b[l];
+            }
+            tot = w == 0 ? a[0] : tot + a[0];
+        }
+        const float r = 1.0f / sqrtf(tot / 2048.0f + eps);
+        for (int c = 0; c < H; ++c) x[c] = (hr[c] * r) * signs[c];
+        fwht_n(x, H);
+        for (int c = 0; c < H; ++c) x[c] = x[c] * INV_SQRT_2048;
+        for (int g = 0; g < H / GROUP; ++g)
+            quant_group_div(x + g * GROUP, q + (size_t)t * H + g * GROUP, s + (size_t)t * (H / GROUP) + g,
+                            sum + (size_t)t * (H / GROUP) + g);
+    }
+}

@@ -79,6 +79,11 @@ int orc_experts(const orc_layer* L, const int8_t* xq, const float* xs, const int
 int orc_reference_f64(const orc_layer* L, const float* x, int T, const int32_t* topk, const float* topw,
                       double* out, int nthreads);
 
+/* Combine + un-rotation + residual add + the next layer's RMSNorm, rotation and A8 (engine/ops.cu:507-549), H = 2048:
+ * h [T, 2048] is updated in place; q/s/sum receive the next layer's A8 input. */
+void orc_combine_norm(const float* Y, const int32_t* tok_slots, int T, int nk, int K1, const float* signs, float eps,
+                      float* h, int8_t* q, float* s, int32_t* sum);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,7 @@ def lib() -> ctypes.CDLL:
         L.orc_experts.restype = i
         L.orc_reference_f64.argtypes = [ctypes.POINTER(OrcLayer), vp, i, vp, vp, vp, i]
         L.orc_reference_f64.restype = i
+        L.orc_combine_norm.argtypes = [vp, vp, i, i, i, vp, f, vp, vp, vp, vp]
         _lib = L
     return _lib
 
@@ -164,6 +165,21 @@ def fwht_a8(Z):
     sm = np.zeros((n, 4), np.int32)
     lib().orc_fwht_a8(_p(Z), n, _p(q), _p(s), _p(sm))
     return q, s, sm
+
+
+def combine_norm(Y, tok_slots, nk, signs, eps, h):
+    """-> (h_new, q, s, sum): combine of the nk first slots of each token, FWHT-2048 un-rotation with signs,
+    residual add into a copy of h, then the next layer's RMSNorm + rotation + A8."""
+    Y = np.ascontiguousarray(Y, np.float32)
+    tok_slots = np.ascontiguousarray(tok_slots, np.int32)
+    T, K1 = tok_slots.shape
+    hn = np.array(h, np.float32, copy=True)
+    q = np.zeros((T, 2048), np.int8)
+    s = np.zeros((T, 16), np.float32)
+    sm = np.zeros((T, 16), np.int32)
+    lib().orc_combine_norm(_p(Y), _p(tok_slots), T, nk, K1, _p(np.ascontiguousarray(signs, np.float32)), eps, _p(hn),
+                           _p(q), _p(s), _p(sm))
+    return hn, q, s, sm
 
 
 class Layer:

@@ -199,6 +199,31 @@ def test_tiled_units_bit_exact(gpu, T, mix, kind):
     G.close()
 
 
+@pytest.mark.parametrize("T,pool", [(32, 256), (200, 48)])
+def test_experts_norm_bit_exact(gpu, T, pool):
+    """llmoe_experts_norm: combine + FWHT-2048 un-rotation + residual + next-layer RMSNorm / rotation / A8."""
+    import torch
+    say(f"[experts_norm] T={T} pool={pool}")
+    L = layer_for("mixed", True)
+    G = make_gpu_layer(L, pool)
+    x = synth.make_x(900 + T, T)
+    signs = np.where(np.random.default_rng(T).random(2048) < 0.5, -1.0, 1.0).astype(np.float32)
+    h0 = (np.random.default_rng(T + 1).standard_normal((T, 2048)) * 2).astype(np.float32)
+    xq, xs, xsum = oracle.quant_a8(x)
+    dx = [to_dev(a, gpu) for a in (xq, xs, xsum)]
+    G.route(T, x=to_dev(x, gpu))
+    h = to_dev(h0, gpu)
+    q, s, sm = G.experts_norm(*dx, to_dev(signs, gpu), 1e-6, h)
+    torch.cuda.synchronize()
+    r = oracle.Layer(L).forward(x, C=pool)
+    hn, rq, rs, rsm = oracle.combine_norm(r["Y"], r["tok_slots"], 9, signs, 1e-6, h0)
+    assert np.array_equal(h.cpu().numpy().view(np.uint32), hn.view(np.uint32)), "residual not bit-exact"
+    assert np.array_equal(q.cpu().numpy(), rq)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+    assert np.array_equal(sm.cpu().numpy(), rsm)
+    G.close()
+
+
 def test_router_logits_bit_exact(gpu):
     T = 70
     say(f"[router logits] T={T}")

@@ -292,3 +292,36 @@ def test_experts_vs_fp64_with_shared():
     for k in range(9):
         acc = acc + r["Y"][r["tok_slots"][:, k]]
     np.testing.assert_array_equal(acc, r["out"])
+
+
+# ---- combine + un-rotation + residual + next-layer norm / rotation / A8 (engine/ops.cu:507-549) ---------------
+def _sylvester(n):
+    H = np.ones((1, 1))
+    while H.shape[0] < n:
+        H = np.block([[H, H], [H, -H]])
+    return H
+
+
+def test_combine_norm_closed_form():
+    T, K1 = 3, 9
+    Y = gen.normal(120, (T * K1, 2048)).astype(np.float32)
+    tok_slots = np.arange(T * K1, dtype=np.int32).reshape(T, K1)[:, ::-1].copy()   # any slot order
+    signs = np.where(gen.uniform(121, (2048,)) < 0.5, -1.0, 1.0).astype(np.float32)
+    h = (gen.normal(122, (T, 2048)) * 3).astype(np.float32)
+    eps = 1e-6
+    hn, q, s, sm = O.combine_norm(Y, tok_slots, 9, signs, eps, h)
+    H = _sylvester(2048)
+    x = Y.astype(np.float64)[tok_slots].sum(1)
+    h64 = h + (x @ H) * signs / np.sqrt(2048)                          # x Q^T, Q = diag(signs) H / sqrt(2048)
+    np.testing.assert_allclose(hn, h64, rtol=0, atol=2e-6 * np.abs(h64).max())
+    y64 = ((hn.astype(np.float64) / np.sqrt((hn.astype(np.float64) ** 2).mean(1, keepdims=True) + eps)) * signs) @ H
+    y64 /= np.sqrt(2048)
+    s64 = np.abs(y64.reshape(T, 16, 128)).max(-1) / 127
+    np.testing.assert_allclose(s, s64, rtol=1e-5)
+    qd = np.rint(y64.reshape(T, 16, 128) / s[:, :, None])
+    assert np.abs(q.reshape(T, 16, 128) - qd).max() <= 1                  # rounding-boundary flips only
+    assert (q.reshape(T, 16, 128) == qd).mean() > 0.999
+    np.testing.assert_array_equal(sm, q.reshape(T, 16, 128).astype(np.int32).sum(-1))
+    # the rotation is orthogonal: ||Q^T v|| = ||v|| (checked on the un-rotation increment)
+    inc = (hn - h).astype(np.float64)
+    np.testing.assert_allclose(np.linalg.norm(inc, axis=1), np.linalg.norm(x, axis=1), rtol=1e-5)
