@@ -18,6 +18,8 @@
  * in-process C++ below its whole-model C ABI engine/libllada.cu:13-52):
  *   llmoe_layer_create    Engine::load's expert part: ExpertTable + relayout_matrix (engine/engine.cu:206-224,
  *                         engine/moe_i8.cu:48-53, :93-121)
+ *   llmoe_layer_load      the same from the on-disk model directory (read_index + Engine::load,
+ *                         engine/engine.cu:54-75, :166-224)
  *   llmoe_quantize_a8     ops::quant_rows_q8 / quant_row_smem (engine/ops.cu:40-66, :127-135)
  *   llmoe_route           ops::router_mma + ops::route_schedule / route_batch_select/plan/place
  *                         (engine/ops.cu:137-205, :223-423)
@@ -164,6 +166,17 @@ int llmoe_layer_time_stage(llmoe_layer* layer, int stage, int reps, llmoe_stream
  * avg_ms = milliseconds per launch. */
 int llmoe_layers_time_stage(llmoe_layer* const* layers, int n, int stage, int reps, llmoe_stream stream,
                             float* avg_ms);
+
+/* Load the MoE half of layer `layer` from the reference's model directory (engine/engine.cu:54-75, :166-224):
+ * engine.idx (C config, T tensors, E experts, F file sizes, quant/s07c_index.py), the routed experts of
+ * experts_L<layer>.bin, the shared expert ("gate_up", "down" of nonexpert_L<layer>.bin, packlib i8 at C
+ * nonexpert_bits), the router (small.bin "L<layer>.router", bf16 [E, H]) and the expert bias (small.bin
+ * "L<layer>.expert_bias", fp32 [E]); pool = C expert_capacity (48), block = C block_size (32). Pruned experts
+ * (bits 0) are rejected. Then as llmoe_layer_create with max_tokens. */
+int llmoe_layer_load(const char* model_dir, int layer, int max_tokens, llmoe_layer** out);
+
+/* The residual-rotation signs (small.bin "signs", fp32 [n], Q = diag(signs) H / sqrt(n)) into host memory. */
+int llmoe_model_signs(const char* model_dir, float* signs, int n);
 
 /* Message of the calling thread's last error ("" if none). */
 const char* llmoe_last_error(void);

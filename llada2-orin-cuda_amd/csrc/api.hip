@@ -47,6 +47,13 @@ bool g_setup_done = false;
 
 }  // namespace
 
+namespace llmoe {
+int set_error(int code, const char* msg) {
+    g_err = msg;
+    return code;
+}
+}  // namespace llmoe
+
 struct llmoe_layer {
     llmoe_layer_desc d{};
     int nexp = 0;                                   // E + has_shared

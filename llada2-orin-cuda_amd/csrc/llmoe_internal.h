@@ -141,6 +141,9 @@ struct GemmArgs {
 
 enum GemmMode { GEMM_GATE_UP = 0, GEMM_DOWN = 1, GEMM_PRODUCTS_GATE_UP = 2, GEMM_PRODUCTS_DOWN = 3 };
 
+// records msg as the calling thread's last error (llmoe_last_error) and returns code
+int set_error(int code, const char* msg);
+
 hipError_t gemm_setup();   // function attributes (dynamic LDS), once per process
 hipError_t launch_expert_gemm(int mode, int nt, const GemmArgs& a, int max_items, hipStream_t st);
 // tiled units (a.items / a.n_items): mode GEMM_GATE_UP or GEMM_DOWN

@@ -63,7 +63,7 @@ EXPORTS = [
     "llmoe_layer_create", "llmoe_layer_destroy", "llmoe_quantize_a8", "llmoe_route", "llmoe_dispatch",
     "llmoe_experts", "llmoe_experts_norm", "llmoe_layer_forward", "llmoe_layer_buffers", "llmoe_layer_weight_bytes",
     "llmoe_group_products", "llmoe_layer_set_profiling", "llmoe_layer_stage_ms", "llmoe_layer_time_stage", "llmoe_layers_time_stage",
-    "llmoe_last_error",
+    "llmoe_layer_load", "llmoe_model_signs", "llmoe_last_error",
 ]
 
 STAGES = ["quant", "router", "route", "dispatch", "gate_up", "fwht", "down", "combine"]
@@ -82,6 +82,8 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib = ctypes.CDLL(str(p))
     vp, i, f, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
     lib.llmoe_last_error.restype = ctypes.c_char_p
+    lib.llmoe_layer_load.argtypes = [ctypes.c_char_p, i, i, ctypes.POINTER(ctypes.c_void_p)]
+    lib.llmoe_model_signs.argtypes = [ctypes.c_char_p, vp, i]
     lib.llmoe_layer_create.argtypes = [ctypes.POINTER(LayerDesc), vp, sz, vp, vp, vp, vp, vp,
                                        ctypes.POINTER(ctypes.c_void_p)]
     lib.llmoe_layer_destroy.argtypes = [vp]
@@ -148,6 +150,18 @@ class Layer:
                                            _ptr(d_off), _ptr(bits), _ptr(rw), _ptr(bias), ctypes.byref(h)))
         self.handle = h
         self.T = None
+
+    @classmethod
+    def load(cls, model_dir, layer: int, max_tokens: int = 4096) -> "Layer":
+        """llmoe_layer_load: the MoE half of `layer` from the reference's model directory."""
+        self = cls.__new__(cls)
+        self.lib = load_library()
+        h = ctypes.c_void_p()
+        _check(self.lib.llmoe_layer_load(str(model_dir).encode(), layer, max_tokens, ctypes.byref(h)))
+        self.handle = h
+        self.T = None
+        self.desc = LayerDesc(2048, 512, 256, 8, 48, 32, 2.5, 1, max_tokens)   # informational
+        return self
 
     def close(self) -> None:
         if getattr(self, "handle", None):

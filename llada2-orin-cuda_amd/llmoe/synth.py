@@ -134,3 +134,62 @@ def logits_skewed(seed: int, T: int, E: int = 256, K: int = 8, hot: int = 16) ->
         lg[t, a] = 4.0 + 0.1 * rng.standard_normal(K // 2)
         lg[t, b] = 4.0 + 0.1 * rng.standard_normal(K - K // 2)
     return lg
+
+
+def bf16_round(a: np.ndarray) -> np.ndarray:
+    """fp32 -> nearest bf16 (ties to even), returned as fp32."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
+    return u.astype(np.uint32).view(np.float32)
+
+
+def write_model_dir(path, layer: dict, li: int = 1, signs=None, extra_cfg=None) -> dict:
+    """Write `layer` in the reference's model-directory format (quant/s07_pack_experts.py, s07b, s07c_index.py):
+    engine.idx, experts_L<li>.bin (routed experts at their blob offsets), nonexpert_L<li>.bin (the shared expert's
+    gate_up / down, 4 KiB aligned) and small.bin (router bf16 [E, H], expert bias, signs). Returns the layer as
+    the loader should see it (router rounded to bf16)."""
+    from pathlib import Path
+    p = Path(path)
+    p.mkdir(parents=True, exist_ok=True)
+    E, H, I = layer["E"], layer["H"], layer["I"]
+    blob = layer["blob"]
+    # routed experts: the blob up to the shared expert's first matrix
+    end = int(min(layer["gu_off"][E], layer["d_off"][E])) if layer["shared"] else blob.size
+    (p / f"experts_L{li}.bin").write_bytes(blob[:end].tobytes())
+    lines = [f"C hidden_size {H}", f"C moe_intermediate_size {I}", f"C num_experts {E}", "C num_experts_per_tok 8",
+             "C expert_capacity 48", "C block_size 32", "C routed_scaling_factor 2.5", "C nonexpert_bits 8"]
+    lines += [f"C {k} {v}" for k, v in (extra_cfg or {}).items()]
+    lines.append(f"F experts_L{li}.bin {end}")
+    for e in range(E):
+        lines.append(f"E {li} {e} {int(layer['bits'][e])} {int(layer['gu_off'][e])} {int(layer['d_off'][e])}")
+
+    def align(f, off):
+        pad = (-off) % 4096
+        f.write(b"\0" * pad)
+        return off + pad
+
+    if layer["shared"]:
+        gu = blob[int(layer["gu_off"][E]):int(layer["gu_off"][E]) + matrix_bytes(2 * I, H, 8)]
+        dn = blob[int(layer["d_off"][E]):int(layer["d_off"][E]) + matrix_bytes(H, I, 8)]
+        with open(p / f"nonexpert_L{li}.bin", "wb") as f:
+            off = 0
+            for name, arr, shape in (("gate_up", gu, (2 * I, H)), ("down", dn, (H, I))):
+                off = align(f, off)
+                f.write(arr.tobytes())
+                lines.append(f"T nonexpert_L{li}.bin {name} {off} {arr.size} i8tiles8 {shape[0]} {shape[1]}")
+                off += arr.size
+    wr = bf16_round(layer["Wr"])
+    if signs is None:
+        signs = np.where(np.random.default_rng(li).random(H) < 0.5, -1.0, 1.0).astype(np.float32)
+    with open(p / "small.bin", "wb") as f:
+        off = 0
+        for name, arr, dt in ((f"L{li}.router", (np.ascontiguousarray(wr.T).view(np.uint32) >> 16).astype(np.uint16), "bf16"),
+                              (f"L{li}.expert_bias", layer["bias"].astype(np.float32), "f32"),
+                              ("signs", np.asarray(signs, np.float32), "f32")):
+            off = align(f, off)
+            f.write(np.ascontiguousarray(arr).tobytes())
+            shape = " ".join(str(s) for s in arr.shape)
+            lines.append(f"T small.bin {name} {off} {arr.nbytes} {dt} {shape}")
+            off += arr.nbytes
+    (p / "engine.idx").write_text("\n".join(lines) + "\n")
+    return dict(layer, Wr=wr, signs=np.asarray(signs, np.float32))

@@ -73,3 +73,40 @@ def test_create_rejects_bad_bits_and_short_blob(lib):
     assert rc == llmoe.LLMOE_EINVAL and "expert 7" in err
     rc, err = _create({}, blob_bytes=1000)
     assert rc == llmoe.LLMOE_EINVAL and "beyond the blob" in err
+
+
+# ---- the model-directory loader (engine/engine.cu:54-75, quant/s07c_index.py) ------------------------------
+def _load(path, layer=1):
+    h = ctypes.c_void_p()
+    rc = llmoe.load_library().llmoe_layer_load(str(path).encode(), layer, 64, ctypes.byref(h))
+    return rc, llmoe.load_library().llmoe_last_error().decode()
+
+
+def test_load_missing_dir(lib, tmp_path):
+    rc, err = _load(tmp_path / "nope")
+    assert rc == llmoe.LLMOE_EINVAL and "engine.idx" in err
+
+
+def test_load_rejects_bad_index(lib, tmp_path):
+    L = llmoe.synth.make_layer(3, E=64, experts=[0], shared=True)
+    llmoe.synth.write_model_dir(tmp_path, L, li=2)
+    idx = (tmp_path / "engine.idx").read_text()
+    rc, err = _load(tmp_path, layer=5)
+    assert rc == llmoe.LLMOE_EINVAL and "layer 5" in err
+    (tmp_path / "engine.idx").write_text(idx.replace("E 2 7 ", "E 2 7 0 ", 1).replace("E 2 7 0 " + idx.split("E 2 7 ")[1].split()[0] + " ", "E 2 7 0 ", 1))
+    rc, err = _load(tmp_path, layer=2)
+    assert rc == llmoe.LLMOE_EINVAL and "pruned" in err
+    (tmp_path / "engine.idx").write_text(idx + "X what\n")
+    rc, err = _load(tmp_path, layer=2)
+    assert rc == llmoe.LLMOE_EINVAL and "unknown line" in err
+    (tmp_path / "engine.idx").write_text(idx.replace(f"F experts_L2.bin ", "F experts_L2.bin 1", 1))
+    rc, err = _load(tmp_path, layer=2)
+    assert rc == llmoe.LLMOE_EINVAL and "engine.idx says" in err
+
+
+def test_model_signs(lib, tmp_path):
+    L = llmoe.synth.make_layer(4, E=64, experts=[0], shared=True)
+    ref = llmoe.synth.write_model_dir(tmp_path, L, li=1)
+    out = np.zeros(2048, np.float32)
+    assert llmoe.load_library().llmoe_model_signs(str(tmp_path).encode(), out.ctypes.data, 2048) == 0
+    np.testing.assert_array_equal(out, ref["signs"])

@@ -224,6 +224,24 @@ def test_experts_norm_bit_exact(gpu, T, pool):
     G.close()
 
 
+def test_layer_load_matches_create(gpu, tmp_path):
+    """llmoe_layer_load from a model directory in the reference's format == llmoe_layer_create on the same data."""
+    say("[load] model dir")
+    L = layer_for("mixed", True)
+    ref = synth.write_model_dir(tmp_path, L, li=3)
+    Gl = Layer.load(tmp_path, 3, max_tokens=64)
+    Gc = Layer(ref["blob"], ref["gu_off"], ref["d_off"], ref["bits"], ref["bias"], ref["Wr"], n_experts=256, top_k=8,
+               pool=48, has_shared=True, max_tokens=64)
+    x = synth.make_x(21, 32)
+    a = run_layer(Gl, x, gpu)
+    b = run_layer(Gc, x, gpu)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    r = oracle.Layer(ref).forward(x, C=48)
+    assert np.array_equal(a.view(np.uint32), r["out"].view(np.uint32))
+    Gl.close()
+    Gc.close()
+
+
 def test_router_logits_bit_exact(gpu):
     T = 70
     say(f"[router logits] T={T}")
