@@ -120,6 +120,29 @@ def one_layer_config(llmoe, synth, torch, name, seed, T, mix, shared, pool, step
     return res, (Ls[0], Gs, x, out, fn)
 
 
+def norm_step(llmoe, torch, Gs, x, steps, warmup):
+    """The layer step with the fused combine epilogue (llmoe_experts_norm): route, experts, combine + FWHT-2048
+    un-rotation + residual add + the next layer's RMSNorm / rotation / A8, cycling through the same layers."""
+    T = x.shape[0]
+    dev = x.device
+    xq, xs, xsum = llmoe.quantize_a8(x)
+    signs = torch.from_numpy(np.where(np.random.default_rng(5).random(H) < 0.5, -1.0, 1.0).astype(np.float32)).to(dev)
+    h = torch.randn((T, H), device=dev)
+    nxt = (torch.empty_like(xq), torch.empty_like(xs), torch.empty_like(xsum))
+
+    def fn(i):
+        G = Gs[i % len(Gs)]
+        G.route(T, x=x)
+        G.experts_norm(xq, xs, xsum, signs, 1e-6, h, out=nxt)
+
+    dt = time_steps(fn, steps, warmup)
+    comb = llmoe.time_stage_layers(Gs, "combine", 20)
+    for G in Gs:   # leave each layer's latest call a plain forward again
+        G.forward(x)
+    return {"ms_per_step": dt / steps * 1e3, "tokens_per_s": T * steps / dt, "combine_norm_ms": comb,
+            "combine_ms": llmoe.time_stage_layers(Gs, "combine", 20)}
+
+
 def stack_config(llmoe, synth, torch, steps, warmup, nlayers=20, T=2048):
     """Config 3: 2048 tokens through 20 independently seeded mixed-bit layers (+ shared), Zipf(1.1) load."""
     dev = torch.device("cuda:0")
@@ -277,6 +300,7 @@ def main():
     c1, (L1, G1s, x1, _, _) = one_layer_config(llmoe, synth, torch, "config 1: 32 tokens, mixed 2/3/4-bit + W8A8 "
                                               "shared, uniform-random routing (no pool)", 1, 32, "mixed", True, 256,
                                               args.steps, args.warmup)
+    c1["with_combine_norm"] = norm_step(llmoe, torch, G1s, x1, args.steps, args.warmup)
     configs = [c1]
     if not args.only_headline:
         log("[bench] config 0")

@@ -156,9 +156,10 @@ int llmoe_group_products(llmoe_layer* layer, int expert, int which, const int8_t
 int llmoe_layer_set_profiling(llmoe_layer* layer, int enabled);
 int llmoe_layer_stage_ms(llmoe_layer* layer, float* ms);
 
-/* Re-launch one expert stage of the latest llmoe_experts call (LLMOE_STAGE_GATE_UP, _FWHT, _DOWN or _COMBINE)
- * `reps` times back to back between two HIP events on `stream`, and return the average milliseconds per
- * launch (the kernel's steady-state duration; the stages are idempotent). Waits for completion. */
+/* Re-launch one expert stage of the latest llmoe_experts / llmoe_experts_norm call (LLMOE_STAGE_GATE_UP, _FWHT,
+ * _DOWN or _COMBINE) `reps` times back to back between two HIP events on `stream`, and return the average
+ * milliseconds per launch (the kernel's steady-state duration). The stages are idempotent except the combine of
+ * an llmoe_experts_norm call, which adds into h again on every repeat. Waits for completion. */
 int llmoe_layer_time_stage(llmoe_layer* layer, int stage, int reps, llmoe_stream stream, float* avg_ms);
 
 /* As llmoe_layer_time_stage over n layers launched in turn (layer 0, 1, .., n-1, repeated `reps` times): with

@@ -54,6 +54,15 @@ int set_error(int code, const char* msg) {
 }
 }  // namespace llmoe
 
+struct NormOut {            // the combine's fused epilogue (llmoe_experts_norm); h == nullptr: plain combine
+    const float* signs;
+    float eps;
+    float* h;
+    int8_t* q;
+    float* s;
+    int32_t* sum;
+};
+
 struct llmoe_layer {
     llmoe_layer_desc d{};
     int nexp = 0;                                   // E + has_shared
@@ -92,6 +101,7 @@ struct llmoe_layer {
     // the latest llmoe_experts launch (for llmoe_layer_time_stage)
     GemmArgs last_gu{}, last_dn{}, last_tgu{}, last_tdn{};
     float* last_out = nullptr;
+    NormOut last_norm{};
     int last_S = 0, last_T = 0, last_nt = 1;
     bool last_tiled = false;
     bool have_last = false;
@@ -384,15 +394,6 @@ int llmoe_dispatch(llmoe_layer* L, const int32_t* topk, const float* topw, int T
 }  // extern "C"
 
 namespace {
-struct NormOut {            // the combine's fused epilogue (llmoe_experts_norm); h == nullptr: plain combine
-    const float* signs;
-    float eps;
-    float* h;
-    int8_t* q;
-    float* s;
-    int32_t* sum;
-};
-
 int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_t* xsum, int T, float* out,
                  const NormOut& no, hipStream_t st) {
     if (T != L->routed_T) return fail(LLMOE_ESTATE, "no routing for T = %d (route or dispatch first)", T);
@@ -433,7 +434,7 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     tg.n_items = L->n_units + 3;
     L->last_dn = g;
     L->last_tdn = tg;
-    L->last_S = S; L->last_T = T; L->last_tiled = L->tiled; L->last_out = out; L->have_last = true;
+    L->last_S = S; L->last_T = T; L->last_tiled = L->tiled; L->last_out = out; L->last_norm = no; L->have_last = true;
     L->mark(LLMOE_STAGE_DOWN, false, st);
     HIPCHECK(launch_gemm(GEMM_DOWN, g, tg, L->tiled, st));
     L->mark(LLMOE_STAGE_DOWN, true, st);
@@ -515,6 +516,10 @@ hipError_t relaunch_stage(llmoe_layer* L, int stage, hipStream_t st) {
         case LLMOE_STAGE_DOWN: return launch_gemm(GEMM_DOWN, L->last_dn, L->last_tdn, L->last_tiled, st);
         case LLMOE_STAGE_FWHT: return launch_fwht_a8(L->Z, L->last_S, L->zq, L->zs, L->zsum, st);
         case LLMOE_STAGE_COMBINE:
+            if (L->last_norm.h)   // re-adds into h: each repeat moves the residual stream on by one more layer
+                return launch_combine_norm(L->Y, L->tok_slots, L->last_T, d.top_k + (d.has_shared ? 1 : 0),
+                                           d.top_k + 1, L->last_norm.signs, L->last_norm.eps, L->last_norm.h,
+                                           L->last_norm.q, L->last_norm.s, L->last_norm.sum, st);
             return launch_combine(L->Y, L->tok_slots, L->last_T, d.hidden, d.top_k + (d.has_shared ? 1 : 0),
                                   d.top_k + 1, L->last_out, st);
         default: return hipErrorInvalidValue;

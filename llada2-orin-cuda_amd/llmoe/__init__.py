@@ -201,14 +201,16 @@ class Layer:
         _check(self.lib.llmoe_experts(self.handle, _ptr(xq), _ptr(xs), _ptr(xsum), T, _ptr(out), _stream(stream)))
         return out
 
-    def experts_norm(self, xq, xs, xsum, signs, eps, h, stream=None):
+    def experts_norm(self, xq, xs, xsum, signs, eps, h, out=None, stream=None):
         """Experts, then un-rotation + residual into h (in place) + the next layer's RMSNorm / rotation / A8.
-        Returns (q_next, s_next, sum_next)."""
+        Returns (q_next, s_next, sum_next), written into `out` when given."""
         import torch
         T = xq.shape[0]
-        q = torch.empty((T, 2048), dtype=torch.int8, device=xq.device)
-        s = torch.empty((T, 16), dtype=torch.float32, device=xq.device)
-        sm = torch.empty((T, 16), dtype=torch.int32, device=xq.device)
+        if out is None:
+            out = (torch.empty((T, 2048), dtype=torch.int8, device=xq.device),
+                   torch.empty((T, 16), dtype=torch.float32, device=xq.device),
+                   torch.empty((T, 16), dtype=torch.int32, device=xq.device))
+        q, s, sm = out
         _check(self.lib.llmoe_experts_norm(self.handle, _ptr(xq), _ptr(xs), _ptr(xsum), T, _ptr(signs), float(eps),
                                            _ptr(h), _ptr(q), _ptr(s), _ptr(sm), _stream(stream)))
         return q, s, sm
@@ -257,6 +259,18 @@ class Layer:
         out = np.empty(shape, dtype=dtype)
         _hip_memcpy_d2h(out, ptr, n)
         return out
+
+
+def quantize_a8(x, stream=None):
+    """llmoe_quantize_a8 of a contiguous fp32 [rows, cols] device tensor: (q int8, s fp32 [rows, cols/128],
+    sum int32 [rows, cols/128])."""
+    import torch
+    rows, cols = x.shape
+    q = torch.empty((rows, cols), dtype=torch.int8, device=x.device)
+    s = torch.empty((rows, cols // 128), dtype=torch.float32, device=x.device)
+    sm = torch.empty((rows, cols // 128), dtype=torch.int32, device=x.device)
+    _check(load_library().llmoe_quantize_a8(_ptr(x), rows, cols, _ptr(q), _ptr(s), _ptr(sm), _stream(stream)))
+    return q, s, sm
 
 
 def time_stage_layers(layers, stage: str, reps: int = 20, stream=None) -> float:
