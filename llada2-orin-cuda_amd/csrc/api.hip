@@ -90,7 +90,9 @@ struct llmoe_layer {
     Item* p_item = nullptr; int* p_count = nullptr;  // unit list of llmoe_group_products
     Item p_item_host[MAX_UNITS_PER_ITEM] = {}; int p_count_host = 1;
     size_t items_cap = 0;                           // work items (before the split into row blocks)
-    size_t chunks_cap = 0;                          // tiled chunks (before the split into row blocks)
+    size_t chunks_cap = 0;                          // tiled chunks
+    int g_gu = 0, g_dn = 0;                         // tiled GEMM grids (workgroups of the work partition)
+    int* tstart = nullptr;                          // [g_gu + 1 + g_dn + 1] tiled work partition
     // routing state
     int routed_T = -1, ntok = 16, max_items = 0;
     bool tiled = false;                             // the routing of routed_T may have tiled units
@@ -169,7 +171,7 @@ int plan_and_place(llmoe_layer* L, const int32_t* topk, const float* topw, int T
     L->mark(LLMOE_STAGE_DISPATCH, false, st);
     HIPCHECK(launch_plan(L->mask, T, d.n_experts, d.top_k, d.block, d.has_shared, L->ntok, L->tiled ? 1 : 0,
                          L->bits_d, L->count, L->start, L->bpre, L->units_gu, L->units_dn, L->tunits_gu,
-                         L->tunits_dn, L->n_units, st));
+                         L->tunits_dn, L->n_units, L->g_gu, L->g_dn, L->tstart, int(L->chunks_cap), st));
     HIPCHECK(launch_place(topk, topw, L->mask, L->bpre, T, d.n_experts, d.top_k, d.block, d.has_shared,
                           L->slot_token, L->slot_weight, L->tok_slots, st));
     L->mark(LLMOE_STAGE_DISPATCH, true, st);
@@ -299,8 +301,14 @@ int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t bl
     ALLOC(L->units_dn, L->items_cap * MAX_UNITS_PER_ITEM);
     ALLOC(L->n_units, 4);
     L->chunks_cap = E + (Tm * K + TILED_NTOK - 1) / TILED_NTOK + (Tm + TILED_NTOK - 1) / TILED_NTOK + 2;
-    ALLOC(L->tunits_gu, L->chunks_cap * MAX_TILED_UNITS_PER_CHUNK);
-    ALLOC(L->tunits_dn, L->chunks_cap * MAX_TILED_UNITS_PER_CHUNK);
+    if ((L->chunks_cap + 1) * sizeof(int) > 65536)
+        return bail(fail(LLMOE_EINVAL, "max_tokens = %d: more tiled chunks than the planner holds", int(Tm)));
+    ALLOC(L->tunits_gu, L->chunks_cap);
+    ALLOC(L->tunits_dn, L->chunks_cap);
+    L->g_gu = tiled_grid(GEMM_GATE_UP);
+    L->g_dn = tiled_grid(GEMM_DOWN);
+    if (L->g_gu < 1 || L->g_dn < 1) return bail(fail(LLMOE_EHIP, "tiled GEMM occupancy query failed"));
+    ALLOC(L->tstart, size_t(L->g_gu + L->g_dn + 2));
     ALLOC(L->slot_token, S);
     ALLOC(L->slot_weight, S);
     ALLOC(L->tok_slots, Tm * (K + 1));
@@ -413,6 +421,7 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     g.K = H; g.R = 2 * I; g.Z = L->Z;
     GemmArgs tg = g;
     tg.items = L->tunits_gu;
+    tg.tstart = L->tstart;
     tg.n_items = L->n_units + 2;
     L->last_gu = g;
     L->last_tgu = tg;
@@ -431,6 +440,7 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     g.K = I; g.R = H; g.Z = nullptr; g.Y = L->Y;
     tg = g;
     tg.items = L->tunits_dn;
+    tg.tstart = L->tstart + L->g_gu + 1;
     tg.n_items = L->n_units + 3;
     L->last_dn = g;
     L->last_tdn = tg;

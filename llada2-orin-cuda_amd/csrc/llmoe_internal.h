@@ -51,7 +51,12 @@ __host__ __device__ constexpr int tiled_chunks(int c) { return (c + TILED_NTOK -
 __host__ __device__ constexpr int tiled_per(int c) {
     return c <= 0 ? 0 : (((c + tiled_chunks(c) - 1) / tiled_chunks(c)) + 15) / 16 * 16;
 }
-constexpr int MAX_TILED_UNITS_PER_CHUNK = 4;    // row-block ranges per chunk (tiled_split)
+// Tiled work partition: the chunks are listed in order, chunk i spanning positions [pre_i, pre_i + 16 ntile_i)
+// (ntile_i = its 16-slot tiles, a cost proportional to its MFMA work in both GEMMs), and its row block r of
+// nrb starting at pre_i + r 16 ntile_i / nrb. Workgroup w of the G-workgroup grid runs the row-block tasks
+// whose start lies in [ceil(w C / G), ceil((w + 1) C / G)), C = the total; tstart[w] = its first task as
+// chunk | rb << TASK_RB_SHIFT (tstart[G] = all chunks, rb 0).
+constexpr int TASK_RB_SHIFT = 20;
 
 // Device weight layout (written by relayout_matrix from packlib "i8"):
 //   matrix [R, K] = R/16 strips of 16 rows; a strip = K/512 superblocks; a superblock (4 groups of 128) =
@@ -137,6 +142,7 @@ struct GemmArgs {
     uint16_t* Z;                // gate_up out [slots, R/2] fp16
     float* Y;                   // down out [slots, R]
     int32_t* P;                 // group-products out [n, R, K/128] (test entry)
+    const int* tstart;          // tiled: [G + 1] first task of each workgroup (the work partition above)
 };
 
 enum GemmMode { GEMM_GATE_UP = 0, GEMM_DOWN = 1, GEMM_PRODUCTS_GATE_UP = 2, GEMM_PRODUCTS_DOWN = 3 };
@@ -148,6 +154,8 @@ hipError_t gemm_setup();   // function attributes (dynamic LDS), once per proces
 hipError_t launch_expert_gemm(int mode, int nt, const GemmArgs& a, int max_items, hipStream_t st);
 // tiled units (a.items / a.n_items): mode GEMM_GATE_UP or GEMM_DOWN
 hipError_t tiled_setup();
+// resident workgroups of the tiled GEMM grid for mode GEMM_GATE_UP / GEMM_DOWN (the G of the work partition)
+int tiled_grid(int mode);
 hipError_t launch_tiled_gemm(int mode, const GemmArgs& a, hipStream_t st);
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, int R, int K, int bits, int gate_up, hipStream_t st);
 hipError_t launch_quant_a8(const float* x, int rows, int cols, int8_t* q, float* s, int* sum, hipStream_t st);
@@ -171,11 +179,15 @@ hipError_t launch_decode_route(const float* part, int nchunks, const float* bias
                                Item* units_gu, Item* units_dn, int* n_units, int32_t* slot_token, float* slot_weight,
                                int32_t* tok_slots, hipStream_t st);
 hipError_t launch_masks(const int32_t* topk, int T, int E, int K, int block, uint32_t* mask, hipStream_t st);
-// work units: streamed units_gu / units_dn (n_units[0] / [1], items of <= ntok slots), tiled tunits_gu /
-// tunits_dn (n_units[2] / [3]) for experts with more than TILED_MIN slots when `tiled` is set
+// work units: streamed units_gu / units_dn (n_units[0] / [1], items of <= ntok slots); when `tiled` is set, the
+// chunks of the experts with more than TILED_MIN slots in tunits_gu / tunits_dn (n_units[2] / [3], Item.rb =
+// the chunk's position pre_i) and the work partition of the two tiled grids (g_gu / g_dn workgroups):
+// tstart[0 .. g_gu] for gate_up, tstart[g_gu + 1 .. g_gu + 1 + g_dn] for down. max_chunks bounds the chunk count
+// (dynamic LDS).
 hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int has_shared, int ntok, int tiled,
                        const int8_t* bits, int32_t* count, int32_t* start, int32_t* bpre, Item* units_gu,
-                       Item* units_dn, Item* tunits_gu, Item* tunits_dn, int* n_units, hipStream_t st);
+                       Item* units_dn, Item* tunits_gu, Item* tunits_dn, int* n_units, int g_gu, int g_dn,
+                       int* tstart, int max_chunks, hipStream_t st);
 hipError_t launch_place(const int32_t* topk, const float* topw, const uint32_t* mask, const int32_t* bpre, int T,
                         int E, int K, int block, int has_shared, int32_t* slot_token, float* slot_weight,
                         int32_t* tok_slots, hipStream_t st);

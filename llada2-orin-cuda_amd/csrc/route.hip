@@ -186,32 +186,32 @@ __device__ void emit_shared_units(int E, int T, int K, int ntok, int bits, Item*
     }
 }
 
-// tiled units of expert e (c slots from slot st): chunks of tiled_per(c) slots, each split into `split` ranges
-// of row blocks (Item.rb = first | count << 16)
-__device__ __forceinline__ int rb_range(int R, int split, int r) { return (r * (R / split)) | ((R / split) << 16); }
-__device__ void emit_tiled_units(int e, int c, int st, int bits, int split, int base_gu, int base_dn, Item* tunits_gu,
-                                 Item* tunits_dn) {
+// tiled chunks of expert e (c slots from slot st): tiled_per(c) slots each, the last one shorter; Item.rb is
+// filled in with the chunk's position once the whole list is written
+__device__ void emit_tiled_units(int e, int c, int st, int base, Item* tunits_gu) {
     const int nch = tiled_chunks(c), per = tiled_per(c);
-    const int rg = tiled_row_blocks(false, bits), rd = tiled_row_blocks(true, bits);
-    for (int j = 0; j < nch; ++j) {
-        const int s0 = st + j * per, n = min(per, c - j * per);
-        for (int r = 0; r < split; ++r) {
-            tunits_gu[base_gu + j * split + r] = Item{e, s0, n, rb_range(rg, split, r)};
-            tunits_dn[base_dn + j * split + r] = Item{e, s0, n, rb_range(rd, split, r)};
-        }
-    }
+    for (int j = 0; j < nch; ++j) tunits_gu[base + j] = Item{e, st + j * per, min(per, c - j * per), 0};
 }
 
-// the shared expert's tiled units (all T tokens, slots T K + t), the first of both tiled lists
-__device__ void emit_shared_tiled_units(int E, int T, int K, int bits, int split, Item* tunits_gu, Item* tunits_dn) {
+// the shared expert's tiled chunks (all T tokens, slots T K + t), the first of the tiled list
+__device__ void emit_shared_tiled_units(int T, int E, int K, Item* tunits_gu) {
     const int nch = tiled_chunks(T), per = tiled_per(T);
-    const int rg = tiled_row_blocks(false, bits), rd = tiled_row_blocks(true, bits);
-    for (int u = threadIdx.x; u < nch * split; u += blockDim.x) {
-        const int j = u / split, r = u % split;
-        const Item it{E, T * K + j * per, min(per, T - j * per), 0};
-        tunits_gu[u] = Item{it.expert, it.slot0, it.ntok, rb_range(rg, split, r)};
-        tunits_dn[u] = Item{it.expert, it.slot0, it.ntok, rb_range(rd, split, r)};
+    for (int j = threadIdx.x; j < nch; j += blockDim.x) tunits_gu[j] = Item{E, T * K + j * per, min(per, T - j * per), 0};
+}
+
+// first row-block task at or after position lo of the chunk list (positions pre[0 .. n], pre[n] = total)
+__device__ int first_task(const int* pre, int n, long long lo, const Item* chunks, const int8_t* bits, bool down) {
+    if (lo >= pre[n]) return n;
+    int a = 0, b = n;                 // pre[a] <= lo < pre[b]
+    while (b - a > 1) {
+        const int m = (a + b) >> 1;
+        if (pre[m] <= lo) a = m;
+        else b = m;
     }
+    const int nrb = tiled_row_blocks(down, bits[chunks[a].expert]);
+    const int span = (pre[a + 1] - pre[a]) / nrb;
+    const int r = int((lo - pre[a] + span - 1) / span);
+    return r >= nrb ? a + 1 : (a | (r << TASK_RB_SHIFT));
 }
 
 struct DispatchOut {         // written by the single-block fused route (decode): the plan + place results
@@ -627,8 +627,10 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
                                                    int* __restrict__ start, int* __restrict__ bpre,
                                                    Item* __restrict__ units_gu, Item* __restrict__ units_dn,
                                                    Item* __restrict__ tunits_gu, Item* __restrict__ tunits_dn,
-                                                   int* __restrict__ n_units) {
+                                                   int* __restrict__ n_units, int g_gu, int g_dn,
+                                                   int* __restrict__ tstart) {
     constexpr int NBR = 64;                    // token masks of the first NBR blocks stay in registers
+    extern __shared__ int pre[];               // chunk positions [n_chunks + 1]
     __shared__ int wt_i[4], wt_c[4];
     __shared__ uint64_t wt[4][4];
     __shared__ uint64_t tot[4];
@@ -647,7 +649,7 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     const int bw = e < E ? bits[e] : 2, cls = width_class(bw);
     const int nit = e < E && !big ? (c + ntok - 1) / ntok : 0, nch = big ? tiled_chunks(c) : 0;
     // one pass of inclusive scans over the experts: slots, tiled chunks, and per width class (16-bit fields) the
-    // streamed and tiled units of both lists; the chunk total decides the row split of the tiled units first
+    // streamed units of both lists and the tiled chunks
     int incl = c, inch = nch;
     uint64_t s0 = uint64_t(nit * gemm_row_blocks(false, bw)) << (16 * cls);
     uint64_t s1 = uint64_t(nit * gemm_row_blocks(true, bw)) << (16 * cls);
@@ -687,23 +689,20 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
         wt_i[0] = inch;            // all routed chunks (read after the barrier below)
     }
     __syncthreads();
-    const int all_chunks = wt_i[0] + nsch;
-    // row-block ranges per chunk: enough tiled units to fill the GPU (split a chunk's rows when chunks are few)
-    const int split = all_chunks >= 384 ? 1 : all_chunks >= 192 ? 2 : 4;
     const int sbits = has_shared ? bits[E] : 8;
     const int ns = has_shared && !sbig ? (T + ntok - 1) / ntok : 0;
     // offsets: the shared expert's units first, then width classes 0 .. 3 (8, 4, 3, 2 bits), expert ascending
-    int bg = ns * gemm_row_blocks(false, sbits), bd = ns * gemm_row_blocks(true, sbits), bt = nsch * split;
+    int bg = ns * gemm_row_blocks(false, sbits), bd = ns * gemm_row_blocks(true, sbits), bt = nsch;
     int og = 0, od = 0, ot = 0;
     for (int k = 0; k < 4; ++k) {
         if (k == cls) {
             og = bg + int(((s0 - own0) >> (16 * k)) & 0xFFFFu);
             od = bd + int(((s1 - own1) >> (16 * k)) & 0xFFFFu);
-            ot = bt + split * int(((t0 - ownt) >> (16 * k)) & 0xFFFFu);
+            ot = bt + int(((t0 - ownt) >> (16 * k)) & 0xFFFFu);
         }
         bg += int((tot[0] >> (16 * k)) & 0xFFFFu);
         bd += int((tot[1] >> (16 * k)) & 0xFFFFu);
-        bt += split * int((tot[2] >> (16 * k)) & 0xFFFFu);
+        bt += int((tot[2] >> (16 * k)) & 0xFFFFu);
     }
     const int st = incl - c;
     if (e < E) {
@@ -720,16 +719,50 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
             bpre[size_t(b) * E + e] = run;
             run += __popc(mask[size_t(b) * E + e]);
         }
-        if (big) emit_tiled_units(e, c, st, bw, split, ot, ot, tunits_gu, tunits_dn);
+        if (big) emit_tiled_units(e, c, st, ot, tunits_gu);
         else emit_units(e, c, st, ntok, bw, og, od, units_gu, units_dn);
     }
     if (ns) emit_shared_units(E, T, K, ntok, sbits, units_gu, units_dn);
-    if (sbig) emit_shared_tiled_units(E, T, K, sbits, split, tunits_gu, tunits_dn);
+    if (sbig) emit_shared_tiled_units(T, E, K, tunits_gu);
     if (e == 0) {
         n_units[0] = bg;
         n_units[1] = bd;
         n_units[2] = bt;
         n_units[3] = bt;
+    }
+    if (!tiled) return;
+    // chunk positions: a scan of 16 ntile over the written list (each thread a run of consecutive chunks)
+    __threadfence_block();
+    __syncthreads();
+    const int n = bt, per = (n + blockDim.x - 1) / blockDim.x, j0 = min(n, e * per), j1 = min(n, j0 + per);
+    int run = 0;
+    for (int j = j0; j < j1; ++j) run += 16 * ((tunits_gu[j].ntok + 15) >> 4);
+    int inc = run;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(inc, o);
+        if (lane >= o) inc += v;
+    }
+    if (lane == 63) wt_i[w] = inc;
+    __syncthreads();
+    for (int i = 0; i < w; ++i) inc += wt_i[i];
+    run = inc - run;
+    for (int j = j0; j < j1; ++j) {
+        pre[j] = run;
+        Item it = tunits_gu[j];
+        it.rb = run;
+        tunits_gu[j] = it;
+        tunits_dn[j] = it;
+        run += 16 * ((it.ntok + 15) >> 4);
+    }
+    if (e == blockDim.x - 1) pre[n] = inc;
+    __syncthreads();
+    const long long total = pre[n];
+    for (int q = e; q <= g_gu + g_dn + 1; q += blockDim.x) {
+        const bool down = q > g_gu;
+        const int wg = down ? q - g_gu - 1 : q, G = down ? g_dn : g_gu;
+        const long long lo = (long long)(wg) * total / G + ((long long)(wg) * total % G != 0);
+        tstart[q] = first_task(pre, n, lo, tunits_gu, bits, down);
     }
 }
 
@@ -809,9 +842,12 @@ hipError_t launch_masks(const int32_t* topk, int T, int E, int K, int block, uin
 
 hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int has_shared, int ntok, int tiled,
                        const int8_t* bits, int32_t* count, int32_t* start, int32_t* bpre, Item* units_gu,
-                       Item* units_dn, Item* tunits_gu, Item* tunits_dn, int* n_units, hipStream_t st) {
-    plan_kernel<<<1, 256, 0, st>>>(mask, T, E, K, block, has_shared, ntok, tiled, bits, count, start, bpre, units_gu,
-                                   units_dn, tunits_gu, tunits_dn, n_units);
+                       Item* units_dn, Item* tunits_gu, Item* tunits_dn, int* n_units, int g_gu, int g_dn,
+                       int* tstart, int max_chunks, hipStream_t st) {
+    plan_kernel<<<1, 256, size_t(max_chunks + 1) * sizeof(int), st>>>(mask, T, E, K, block, has_shared, ntok, tiled,
+                                                                     bits, count, start, bpre, units_gu, units_dn,
+                                                                     tunits_gu, tunits_dn, n_units, g_gu, g_dn,
+                                                                     tstart);
     return hipGetLastError();
 }
 

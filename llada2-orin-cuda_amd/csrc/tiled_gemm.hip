@@ -10,9 +10,9 @@
 // into MFMA A operands and used for all 4 token tiles, and the fp32 accumulators of the (strip, token tile)
 // pairs stay in registers until the fused epilogue. No barrier inside a row block, so the 8 waves (2 per SIMD)
 // drift freely and one wave's MFMAs overlap the other's vector epilogue.
-// Zero points: for 2/3/4-bit codes the zero is subtracted while unpacking (c - z fits int8), so the MFMA
-// accumulates from 0 and no per-element integer work remains; 8-bit codes (stored c - 128) keep the
-// zero term zero' * (-Sxq) as the MFMA's initial accumulator.
+// Zero points: for 2/3-bit codes the zero is subtracted while unpacking (a v_perm_b32 lookup of c - z), so the
+// MFMA accumulates from 0; 4-bit codes and 8-bit codes (stored c - 128) start the MFMA from the zero term
+// zero * (-Sxq) of the lane's four output rows instead.
 #include <type_traits>
 
 #include "llmoe_internal.h"
@@ -30,9 +30,8 @@ constexpr int MAX_TILE = TILED_NTOK / 16;       // 16-token tiles per chunk
 // LDS: activations [group][token][128 B] (16-byte chunk c of token n at ((c ^ (n & 7)) * 16)), then fp32 scales
 // and negated int32 sums [group][token], then the chunk's row table [token]
 constexpr int GROUP_B = TILED_NTOK * GROUP;
-constexpr int PF_SCRATCH = 1024;                // per wave: LDS target of the L2 prefetches (never read)
 __host__ __device__ constexpr int lds_bytes_for(int K) {
-    return (K / GROUP) * (GROUP_B + TILED_NTOK * 8) + TILED_NTOK * 4 + NW * PF_SCRATCH;
+    return (K / GROUP) * (GROUP_B + TILED_NTOK * 8) + TILED_NTOK * 4;
 }
 constexpr int LDS_BYTES = lds_bytes_for(2048);
 
@@ -56,7 +55,7 @@ struct Codes {
 };
 struct Late {
     u4 s1;          // fp16 scales [tile 2-3][rows 4q .. 4q+3]
-    u4 z;           // zeros: BITS < 8 the lane's A-operand row (byte r%4 of dword tile), 8-bit its 4 output rows
+    u4 z;           // zeros: 2/3-bit the lane's A-operand row (byte r%4 of dword tile), 4/8-bit its 4 output rows
     u4 hi;          // 3-bit high plane
 };
 
@@ -72,13 +71,15 @@ template <int BITS>
 __device__ __forceinline__ void load_late(const uint8_t* p, int lane, Late& r) {
     const uint8_t* m = p + BITS * 1024;
     r.s1 = *reinterpret_cast<const u4*>(m + 32 * (lane >> 4) + 16);
-    r.z = *reinterpret_cast<const u4*>(m + 128 + 16 * (BITS == 8 ? (lane >> 4) : ((lane & 15) >> 2)));
+    r.z = *reinterpret_cast<const u4*>(m + 128 + 16 * (BITS >= 4 ? (lane >> 4) : ((lane & 15) >> 2)));
     if constexpr (BITS == 3) r.hi = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p + 2 * 1024) + lane);
 }
 
-// A operand dwords of tile tau (D[0..3]: columns 0..63, D[4..7]: 64..127), zero subtracted for BITS < 8:
-// (c | 0x80) - z per byte never borrows across bytes (c + 128 - z > 0), and ^ 0x80 turns the biased byte into
-// the two's complement of c - z.
+// A operand dwords of tile tau (D[0..3]: columns 0..63, D[4..7]: 64..127). 2/3-bit: the codes select bytes of a
+// table holding c - z for every code c (v_perm_b32). The 2-bit table is the 4-byte window at offset 3 - z of
+// the byte sequence -3 .. 3 (one v_alignbyte_b32); the 3-bit table is built as (c | 0x80) - z per byte, which
+// never borrows across bytes (c + 128 - z > 0), with ^ 0x80 turning the biased byte into the two's complement
+// of c - z. 4/8-bit: the codes as they are (the zero term is on the accumulator).
 template <int BITS>
 __device__ __forceinline__ void unpack_a(const Codes<BITS>& r, const Late& lt, int tau, int lane, uint32_t (&D)[8]) {
     if constexpr (BITS == 8) {
@@ -104,12 +105,20 @@ __device__ __forceinline__ void unpack_a(const Codes<BITS>& r, const Late& lt, i
                     D[s] |= hb & 0x04040404u;
                 }
             }
-            const uint32_t z = (lt.z[tau] >> (8 * (lane & 3))) & 0xFFu;
-            const uint32_t zb = z * 0x01010101u;
-            const uint32_t t_lo = ((0x03020100u | 0x80808080u) - zb) ^ 0x80808080u;   // c - z, c = 0 .. 3
-            const uint32_t t_hi = ((0x07060504u | 0x80808080u) - zb) ^ 0x80808080u;   // c = 4 .. 7
+            if constexpr (BITS == 2) {
+                // alignbyte reads only bits 1:0 of the shift: (z ^ 3) = 3 - z for z in 0 .. 3
+                const uint32_t sh = (lt.z[tau] >> (8 * (lane & 3))) ^ 3u;
+                const uint32_t t = __builtin_amdgcn_alignbyte(0x00030201u, 0x00FFFEFDu, sh);   // c - z, c = 0 .. 3
 #pragma unroll
-            for (int s = 0; s < 8; ++s) D[s] = __builtin_amdgcn_perm(t_hi, t_lo, D[s]);
+                for (int s = 0; s < 8; ++s) D[s] = __builtin_amdgcn_perm(0u, t, D[s]);
+            } else {
+                const uint32_t z = (lt.z[tau] >> (8 * (lane & 3))) & 0xFFu;
+                const uint32_t zb = z * 0x01010101u;
+                const uint32_t t_lo = ((0x03020100u | 0x80808080u) - zb) ^ 0x80808080u;   // c - z, c = 0 .. 3
+                const uint32_t t_hi = ((0x07060504u | 0x80808080u) - zb) ^ 0x80808080u;   // c = 4 .. 7
+#pragma unroll
+                for (int s = 0; s < 8; ++s) D[s] = __builtin_amdgcn_perm(t_hi, t_lo, D[s]);
+            }
             return;
         } else {
             const u4& u = r.c[tau];
@@ -119,10 +128,6 @@ __device__ __forceinline__ void unpack_a(const Codes<BITS>& r, const Late& lt, i
                 D[2 * m + 1] = (u[m] >> 4) & 0x0F0F0F0Fu;
             }
         }
-        const uint32_t z = (lt.z[tau] >> (8 * (lane & 3))) & 0xFFu;
-        const uint32_t zb = z * 0x01010101u;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) D[s] = ((D[s] | 0x80808080u) - zb) ^ 0x80808080u;
     }
 }
 
@@ -146,24 +151,6 @@ __device__ __forceinline__ float mul_f16_f32(uint32_t packed, int hi, float x) {
     if (hi) asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(x), "v"(-0.0f));
     else asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(x), "v"(-0.0f));
     return r;
-}
-
-// Pull 1 KiB (64 lanes x 16 B at p + 16 lane) into the L2 cache ahead of its register loads: an LDS-DMA load into
-// a per-wave scratch area of LDS that nothing reads. It holds no registers, so the prefetch can run superblocks
-// ahead of the register stream; the compiler does not see it, and its own wait counts stay conservative (the
-// hardware counter only ever holds more outstanding loads than the compiler assumes).
-__device__ __forceinline__ void l2_prefetch_kb(const uint8_t* p, uint32_t lds_scratch, int lane) {
-    const void* g = p + 16 * lane;
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_scratch)
-                 : "memory", "m0");
-}
-
-// prefetch one strip-superblock (codes and group parameters) of BITS-bit codes
-template <int BITS>
-__device__ __forceinline__ void prefetch_sb(const uint8_t* p, uint32_t lds_scratch, int lane) {
-#pragma unroll
-    for (int i = 0; i < BITS; ++i) l2_prefetch_kb(p + i * 1024, lds_scratch, lane);
-    l2_prefetch_kb(p + BITS * 1024 - 832, lds_scratch, lane);   // the 1 KiB ending with the 192 B of parameters
 }
 
 // The chunk's activations for the whole reduction -> LDS (all threads; rows of absent tokens are zero, so their
@@ -225,23 +212,9 @@ __device__ __forceinline__ void stage_chunk(const GemmArgs& a, const Item& it, u
 }
 
 // One row block: wave w computes strips (rb * NW + w) * S .. + S - 1 for the chunk staged in LDS.
-// L2 prefetch distance in steps (one step = one superblock of the wave's strips, row blocks in sequence)
-constexpr int PF_STEPS = 2;
-
-template <int BITS, int MODE>
-__device__ __forceinline__ void prefetch_step(const GemmArgs& a, const Item& it, int rb, int sb, uint32_t scratch) {
-    constexpr int NSB = MODE == GEMM_DOWN ? 1 : 4, S = tiled_spw(BITS);
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint8_t* mat = a.base + a.off[it.expert];
-#pragma unroll
-    for (int s = 0; s < S; ++s)
-        prefetch_sb<BITS>(mat + (size_t((rb * NW + wave) * S + s) * NSB + sb) * sb_bytes(BITS), scratch, lane);
-}
-
 template <int BITS, int MODE, int NTILE>
-__device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it, const uint8_t* lds, int rb,
-                                               int rb_end, uint32_t scratch) {
+__device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it, const uint8_t* mat,
+                                               const uint8_t* lds, int rb) {
     constexpr bool DOWN = MODE == GEMM_DOWN;
     constexpr int NSB = DOWN ? 1 : 4, K = NSB * SB_K, G = K / GROUP;
     constexpr int S = tiled_spw(BITS);
@@ -249,7 +222,6 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
     const int lane = threadIdx.x & 63, q = lane >> 4, col = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int strip0 = (rb * NW + wave) * S;
-    const uint8_t* mat = a.base + a.off[it.expert];
     auto sbp = [&](int s, int sb) { return mat + (size_t(strip0 + s) * NSB + sb) * SBB; };
     const float* ss = reinterpret_cast<const float*>(lds + G * GROUP_B);
     const int* sq = reinterpret_cast<const int*>(ss + G * TILED_NTOK);
@@ -275,11 +247,6 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
     static_for<0, G>([&](auto gc) {
         constexpr int g = decltype(gc)::value, sb = g / 4, tau = g % 4;
         const uint8_t* bg = lds + g * GROUP_B;
-        if constexpr (tau == 0) {   // L2 prefetch PF_STEPS superblocks ahead, across row blocks
-            constexpr int t = sb + PF_STEPS;
-            const int prb = rb + t / NSB;
-            if (prb < rb_end) prefetch_step<BITS, MODE>(a, it, prb, t % NSB, scratch);
-        }
         v4i A0[S], A1[S];
         uint32_t swp[S][2];
         int zz[S][4];
@@ -293,9 +260,9 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
             const u4& sv = tau < 2 ? cd[s].s0 : l.s1;
             swp[s][0] = sv[(tau & 1) * 2];
             swp[s][1] = sv[(tau & 1) * 2 + 1];
-            if constexpr (BITS == 8) {
+            if constexpr (BITS >= 4) {
 #pragma unroll
-                for (int v = 0; v < 4; ++v) zz[s][v] = int((l.z[tau] >> (8 * v)) & 0xFFu) - 128;
+                for (int v = 0; v < 4; ++v) zz[s][v] = int((l.z[tau] >> (8 * v)) & 0xFFu) - (BITS == 8 ? 128 : 0);
             }
             // registers tile tau alone used: refill with the next superblock; after the last tile the
             // superblock-wide registers take the superblock after next
@@ -313,7 +280,7 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
         v4i Bn0 = *bptr(0, 0), Bn1 = *bptr(0, 1);
         float xsnext = ss[g * TILED_NTOK + col];
         int nsnext = 0;
-        if constexpr (BITS == 8) nsnext = sq[g * TILED_NTOK + col];
+        if constexpr (BITS >= 4) nsnext = sq[g * TILED_NTOK + col];
         static_for<0, NTILE + 1>([&](auto tc) {
             constexpr int nt = decltype(tc)::value;
             v4i Cc[S];
@@ -326,11 +293,11 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
                     Bn0 = *bptr(nt + 1, 0);
                     Bn1 = *bptr(nt + 1, 1);
                     xsnext = ss[g * TILED_NTOK + (nt + 1) * 16 + col];
-                    if constexpr (BITS == 8) nsnext = sq[g * TILED_NTOK + (nt + 1) * 16 + col];
+                    if constexpr (BITS >= 4) nsnext = sq[g * TILED_NTOK + (nt + 1) * 16 + col];
                 }
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
-                    if constexpr (BITS == 8)
+                    if constexpr (BITS >= 4)
                         Cc[s] = v4i{__mul24(zz[s][0], nsum), __mul24(zz[s][1], nsum), __mul24(zz[s][2], nsum),
                                     __mul24(zz[s][3], nsum)};
                     else
@@ -385,52 +352,78 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
     }
 }
 
+#ifdef LLMOE_TILED_TRACE
+// timing build only: per unit, [start, staged, end, unit | expert << 20 | hw_id << 32] in the 100 MHz clock
+constexpr int TRACE_MAX = 1 << 16;
+__device__ unsigned long long g_trace[TRACE_MAX * 4];
+__device__ __forceinline__ void trace_put(int slot, unsigned long long v) {
+    if (threadIdx.x == 0 && slot < TRACE_MAX * 4) g_trace[slot] = v;
+}
+#define TRACE_AT(u, k) trace_put(4 * (u) + (k), __builtin_amdgcn_s_memrealtime())
+#else
+#define TRACE_AT(u, k) ((void)0)
+#endif
+
 template <int BITS, int MODE, int NTILE>
-__device__ __forceinline__ void tiled_body(const GemmArgs& a, const Item& it, uint8_t* lds) {
+__device__ __forceinline__ void tiled_body(const GemmArgs& a, const Item& it, uint8_t* lds, int rb0, int rb1, int u) {
     constexpr int K = MODE == GEMM_DOWN ? 512 : 2048;
-    constexpr int NSB = K / SB_K;
-    const int rb0 = it.rb & 0xFFFF, nrb = it.rb >> 16;
-    typedef __attribute__((address_space(3))) uint8_t* lds_p;
-    const uint32_t scratch = __builtin_amdgcn_readfirstlane(
-        uint32_t(size_t((lds_p)(lds + lds_bytes_for(K) - NW * PF_SCRATCH + (threadIdx.x >> 6) * PF_SCRATCH))));
-    // the first PF_STEPS steps of the wave's stream, before the activations are staged
-#pragma unroll
-    for (int t = 0; t < PF_STEPS; ++t)
-        if (rb0 + t / NSB < rb0 + nrb) prefetch_step<BITS, MODE>(a, it, rb0 + t / NSB, t % NSB, scratch);
+    (void)u;
+    // the expert's matrix, wave-uniform (one load per unit, not one per row block)
+    const uint64_t mo = a.off[it.expert];
+    const uint8_t* mat = a.base + ((uint64_t(__builtin_amdgcn_readfirstlane(uint32_t(mo >> 32))) << 32) |
+                                   __builtin_amdgcn_readfirstlane(uint32_t(mo)));
     stage_chunk<K>(a, it, lds);
-    for (int rb = rb0; rb < rb0 + nrb; ++rb) tiled_rowblock<BITS, MODE, NTILE>(a, it, lds, rb, rb0 + nrb, scratch);
+    TRACE_AT(u, 1);
+    for (int rb = rb0; rb < rb1; ++rb) tiled_rowblock<BITS, MODE, NTILE>(a, it, mat, lds, rb);
 }
 
+// Workgroup w runs the row-block tasks tstart[w] .. tstart[w + 1] (chunk-major, so the chunk's activations are
+// staged once per run of its row blocks).
 template <int MODE>
 __global__ void __launch_bounds__(NTHREADS) tiled_gemm(GemmArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const int n = *a.n_items;
-    for (int u = blockIdx.x; u < n; u += gridDim.x) {
-        const Item it = a.items[u];
+    constexpr int CMASK = (1 << TASK_RB_SHIFT) - 1;
+    const int s0 = a.tstart[blockIdx.x], s1 = a.tstart[blockIdx.x + 1];
+    const int c0 = s0 & CMASK, r0 = s0 >> TASK_RB_SHIFT, c1 = s1 & CMASK, r1 = s1 >> TASK_RB_SHIFT;
+    int u = blockIdx.x * 16;   // trace slot (timing builds)
+    for (int c = c0; c < c1 || (c == c1 && r1 > 0); ++c) {
+        const Item it = a.items[c];
         const int bits = a.bits[it.expert];
+        const int rb0 = c == c0 ? r0 : 0, rb1 = c == c1 ? r1 : tiled_row_blocks(MODE == GEMM_DOWN, bits);
+        if (rb0 >= rb1) continue;
+#ifdef LLMOE_TILED_TRACE
+        TRACE_AT(u, 0);
+        {
+            unsigned hw;
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+            trace_put(4 * u + 3, (unsigned long long)(c | (it.expert << 20)) | ((unsigned long long)hw << 32));
+        }
+#endif
         // token tiles actually present (a chunk has <= 64 slots; absent tiles are not computed)
         const int nt = (it.ntok + 15) >> 4;
 #ifdef TILED_ONLY
-        tiled_body<TILED_ONLY, MODE, 4>(a, it, lds);
+        tiled_body<TILED_ONLY, MODE, 4>(a, it, lds, rb0, rb1, u);
 #else
         if (nt > 3) {
-            if (bits == 2) tiled_body<2, MODE, 4>(a, it, lds);
-            else if (bits == 3) tiled_body<3, MODE, 4>(a, it, lds);
-            else if (bits == 4) tiled_body<4, MODE, 4>(a, it, lds);
-            else tiled_body<8, MODE, 4>(a, it, lds);
+            if (bits == 2) tiled_body<2, MODE, 4>(a, it, lds, rb0, rb1, u);
+            else if (bits == 3) tiled_body<3, MODE, 4>(a, it, lds, rb0, rb1, u);
+            else if (bits == 4) tiled_body<4, MODE, 4>(a, it, lds, rb0, rb1, u);
+            else tiled_body<8, MODE, 4>(a, it, lds, rb0, rb1, u);
         } else if (nt == 3) {
-            if (bits == 2) tiled_body<2, MODE, 3>(a, it, lds);
-            else if (bits == 3) tiled_body<3, MODE, 3>(a, it, lds);
-            else if (bits == 4) tiled_body<4, MODE, 3>(a, it, lds);
-            else tiled_body<8, MODE, 3>(a, it, lds);
+            if (bits == 2) tiled_body<2, MODE, 3>(a, it, lds, rb0, rb1, u);
+            else if (bits == 3) tiled_body<3, MODE, 3>(a, it, lds, rb0, rb1, u);
+            else if (bits == 4) tiled_body<4, MODE, 3>(a, it, lds, rb0, rb1, u);
+            else tiled_body<8, MODE, 3>(a, it, lds, rb0, rb1, u);
         } else {
-            if (bits == 2) tiled_body<2, MODE, 2>(a, it, lds);
-            else if (bits == 3) tiled_body<3, MODE, 2>(a, it, lds);
-            else if (bits == 4) tiled_body<4, MODE, 2>(a, it, lds);
-            else tiled_body<8, MODE, 2>(a, it, lds);
+            if (bits == 2) tiled_body<2, MODE, 2>(a, it, lds, rb0, rb1, u);
+            else if (bits == 3) tiled_body<3, MODE, 2>(a, it, lds, rb0, rb1, u);
+            else if (bits == 4) tiled_body<4, MODE, 2>(a, it, lds, rb0, rb1, u);
+            else tiled_body<8, MODE, 2>(a, it, lds, rb0, rb1, u);
         }
 #endif
-        __syncthreads();   // the next unit re-stages the activations
+        __syncthreads();   // the next chunk re-stages the activations
+        TRACE_AT(u, 2);
+        ++u;
     }
 }
 
@@ -438,16 +431,25 @@ template <int MODE>
 const void* kptr() { return reinterpret_cast<const void*>(&tiled_gemm<MODE>); }
 
 template <int MODE>
-hipError_t launch_t(const GemmArgs& a, hipStream_t st) {
+int grid_t() {
     static int grid = 0;
     if (!grid) {
         int dev = 0, cus = 0, per_cu = 0;
         hipError_t e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kptr<MODE>(), NTHREADS, lds_bytes_for(MODE == GEMM_DOWN ? 512 : 2048));
-        if (e != hipSuccess) return e;
+        if (e == hipSuccess)
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kptr<MODE>(), NTHREADS,
+                                                             lds_bytes_for(MODE == GEMM_DOWN ? 512 : 2048));
+        if (e != hipSuccess) return 0;
         grid = cus * (per_cu > 0 ? per_cu : 1);
     }
+    return grid;
+}
+
+template <int MODE>
+hipError_t launch_t(const GemmArgs& a, hipStream_t st) {
+    const int grid = grid_t<MODE>();
+    if (!grid) return hipErrorInvalidDevice;
     tiled_gemm<MODE><<<grid, NTHREADS, lds_bytes_for(MODE == GEMM_DOWN ? 512 : 2048), st>>>(a);
     return hipGetLastError();
 }
@@ -460,6 +462,8 @@ hipError_t tiled_setup() {
     return e;
 }
 
+int tiled_grid(int mode) { return mode == GEMM_DOWN ? grid_t<GEMM_DOWN>() : grid_t<GEMM_GATE_UP>(); }
+
 hipError_t launch_tiled_gemm(int mode, const GemmArgs& a, hipStream_t st) {
     if (mode == GEMM_GATE_UP) return launch_t<GEMM_GATE_UP>(a, st);
     if (mode == GEMM_DOWN) return launch_t<GEMM_DOWN>(a, st);
@@ -467,3 +471,15 @@ hipError_t launch_tiled_gemm(int mode, const GemmArgs& a, hipStream_t st) {
 }
 
 }  // namespace llmoe
+
+#ifdef LLMOE_TILED_TRACE
+extern "C" int llmoe_tiled_trace(void* host, size_t bytes, int clear) {
+    if (hipMemcpyFromSymbol(host, HIP_SYMBOL(llmoe::g_trace), bytes) != hipSuccess) return -1;
+    if (clear) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(llmoe::g_trace)) != hipSuccess) return -1;
+        if (hipMemset(p, 0, bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) return -1;
+    }
+    return 0;
+}
+#endif
