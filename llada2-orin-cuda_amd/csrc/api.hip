@@ -159,9 +159,8 @@ int check_T(const llmoe_layer* L, int T) {
 
 // expert GEMMs of one stage: the streamed units, then (if the routing may have any) the tiled units
 hipError_t launch_gemm(int mode, const GemmArgs& g, const GemmArgs& tg, bool tiled, hipStream_t st) {
-    hipError_t e = launch_expert_gemm(mode, 1, g, 0, st);
-    if (e == hipSuccess && tiled) e = launch_tiled_gemm(mode, tg, st);
-    return e;
+    // tiled (T > one routing block): every expert's slots are tiled chunks, the streamed lists are empty
+    return tiled ? launch_tiled_gemm(mode, tg, st) : launch_expert_gemm(mode, 1, g, 0, st);
 }
 
 int plan_and_place(llmoe_layer* L, const int32_t* topk, const float* topw, int T, hipStream_t st) {
@@ -301,7 +300,7 @@ int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t bl
     ALLOC(L->units_dn, L->items_cap * MAX_UNITS_PER_ITEM);
     ALLOC(L->n_units, 4);
     L->chunks_cap = E + (Tm * K + TILED_NTOK - 1) / TILED_NTOK + (Tm + TILED_NTOK - 1) / TILED_NTOK + 2;
-    if ((L->chunks_cap + 1) * sizeof(int) > 65536)
+    if (2 * (L->chunks_cap + 1) * sizeof(int) > 65536)
         return bail(fail(LLMOE_EINVAL, "max_tokens = %d: more tiled chunks than the planner holds", int(Tm)));
     ALLOC(L->tunits_gu, L->chunks_cap);
     ALLOC(L->tunits_dn, L->chunks_cap);

@@ -199,8 +199,20 @@ __device__ void emit_shared_tiled_units(int T, int E, int K, Item* tunits_gu) {
     for (int j = threadIdx.x; j < nch; j += blockDim.x) tunits_gu[j] = Item{E, T * K + j * per, min(per, T - j * per), 0};
 }
 
+// Cost of one row-block task of a chunk with nt 16-slot tiles, in 50 ns units: a per-row-block part (code
+// unpacking, the weight stream) plus a per-tile part (MFMAs and the fp32 epilogue), as measured on MI355X for
+// each code width (8-bit row blocks have half the rows)
+__device__ __forceinline__ int rb_cost(int bits, int nt, bool down) {
+    if (down) return bits == 8 ? 42 + 10 * nt : bits == 3 ? 42 + 21 * nt : bits == 4 ? 48 + 20 * nt : 36 + 20 * nt;
+    return bits == 8 ? 64 + 35 * nt : bits == 3 ? 134 + 66 * nt : bits == 4 ? 78 + 72 * nt : 70 + 70 * nt;
+}
+__device__ __forceinline__ int chunk_cost(const Item& it, const int8_t* bits, bool down) {
+    const int b = bits[it.expert];
+    return tiled_row_blocks(down, b) * rb_cost(b, (it.ntok + 15) >> 4, down);
+}
+
 // first row-block task at or after position lo of the chunk list (positions pre[0 .. n], pre[n] = total)
-__device__ int first_task(const int* pre, int n, long long lo, const Item* chunks, const int8_t* bits, bool down) {
+__device__ int first_task(const int* pre, int n, int lo, const Item* chunks, const int8_t* bits, bool down) {
     if (lo >= pre[n]) return n;
     int a = 0, b = n;                 // pre[a] <= lo < pre[b]
     while (b - a > 1) {
@@ -210,7 +222,7 @@ __device__ int first_task(const int* pre, int n, long long lo, const Item* chunk
     }
     const int nrb = tiled_row_blocks(down, bits[chunks[a].expert]);
     const int span = (pre[a + 1] - pre[a]) / nrb;
-    const int r = int((lo - pre[a] + span - 1) / span);
+    const int r = (lo - pre[a] + span - 1) / span;
     return r >= nrb ? a + 1 : (a | (r << TASK_RB_SHIFT));
 }
 
@@ -630,7 +642,7 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
                                                    int* __restrict__ n_units, int g_gu, int g_dn,
                                                    int* __restrict__ tstart) {
     constexpr int NBR = 64;                    // token masks of the first NBR blocks stay in registers
-    extern __shared__ int pre[];               // chunk positions [n_chunks + 1]
+    extern __shared__ int pre[];               // chunk positions [2][n_chunks + 1] (gate_up, down)
     __shared__ int wt_i[4], wt_c[4];
     __shared__ uint64_t wt[4][4];
     __shared__ uint64_t tot[4];
@@ -643,8 +655,8 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     for (int j = 0; j < NBR; ++j) c += __popc(mv[j]);
     if (e < E)
         for (int b = NBR; b < nb; ++b) c += __popc(mask[size_t(b) * E + e]);
-    const bool big = e < E && tiled && c > TILED_MIN;
-    const bool sbig = has_shared && tiled && T > TILED_MIN;
+    const bool big = e < E && tiled && c > 0;
+    const bool sbig = has_shared && tiled;
     const int nsch = sbig ? tiled_chunks(T) : 0;
     const int bw = e < E ? bits[e] : 2, cls = width_class(bw);
     const int nit = e < E && !big ? (c + ntok - 1) / ntok : 0, nch = big ? tiled_chunks(c) : 0;
@@ -731,38 +743,60 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
         n_units[3] = bt;
     }
     if (!tiled) return;
-    // chunk positions: a scan of 16 ntile over the written list (each thread a run of consecutive chunks)
+    // chunk positions of both GEMMs: scans of the chunk costs over the written list (each thread a run of
+    // consecutive chunks)
     __threadfence_block();
     __syncthreads();
     const int n = bt, per = (n + blockDim.x - 1) / blockDim.x, j0 = min(n, e * per), j1 = min(n, j0 + per);
-    int run = 0;
-    for (int j = j0; j < j1; ++j) run += 16 * ((tunits_gu[j].ntok + 15) >> 4);
-    int inc = run;
+    int run0 = 0, run1 = 0;
+    for (int j = j0; j < j1; ++j) {
+        const Item it = tunits_gu[j];
+        run0 += chunk_cost(it, bits, false);
+        run1 += chunk_cost(it, bits, true);
+    }
+    int inc0 = run0, inc1 = run1;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const int v = __shfl_up(inc, o);
-        if (lane >= o) inc += v;
+        const int v0 = __shfl_up(inc0, o), v1 = __shfl_up(inc1, o);
+        if (lane >= o) {
+            inc0 += v0;
+            inc1 += v1;
+        }
     }
-    if (lane == 63) wt_i[w] = inc;
+    if (lane == 63) {
+        wt_i[w] = inc0;
+        wt_c[w] = inc1;
+    }
     __syncthreads();
-    for (int i = 0; i < w; ++i) inc += wt_i[i];
-    run = inc - run;
+    for (int i = 0; i < w; ++i) {
+        inc0 += wt_i[i];
+        inc1 += wt_c[i];
+    }
+    int* pre_dn = pre + n + 1;
+    run0 = inc0 - run0;
+    run1 = inc1 - run1;
     for (int j = j0; j < j1; ++j) {
-        pre[j] = run;
         Item it = tunits_gu[j];
-        it.rb = run;
+        pre[j] = run0;
+        pre_dn[j] = run1;
+        run0 += chunk_cost(it, bits, false);
+        run1 += chunk_cost(it, bits, true);
+        it.rb = pre[j];
         tunits_gu[j] = it;
+        it.rb = pre_dn[j];
         tunits_dn[j] = it;
-        run += 16 * ((it.ntok + 15) >> 4);
     }
-    if (e == blockDim.x - 1) pre[n] = inc;
+    if (e == blockDim.x - 1) {
+        pre[n] = inc0;
+        pre_dn[n] = inc1;
+    }
     __syncthreads();
-    const long long total = pre[n];
     for (int q = e; q <= g_gu + g_dn + 1; q += blockDim.x) {
         const bool down = q > g_gu;
         const int wg = down ? q - g_gu - 1 : q, G = down ? g_dn : g_gu;
-        const long long lo = (long long)(wg) * total / G + ((long long)(wg) * total % G != 0);
-        tstart[q] = first_task(pre, n, lo, tunits_gu, bits, down);
+        const int* P = down ? pre_dn : pre;
+        const long long total = P[n], x = (long long)(wg) * total;
+        tstart[q] = first_task(P, n, int(x / G + (x % G != 0)), tunits_gu, bits, down);
     }
 }
 
@@ -844,7 +878,7 @@ hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int
                        const int8_t* bits, int32_t* count, int32_t* start, int32_t* bpre, Item* units_gu,
                        Item* units_dn, Item* tunits_gu, Item* tunits_dn, int* n_units, int g_gu, int g_dn,
                        int* tstart, int max_chunks, hipStream_t st) {
-    plan_kernel<<<1, 256, size_t(max_chunks + 1) * sizeof(int), st>>>(mask, T, E, K, block, has_shared, ntok, tiled,
+    plan_kernel<<<1, 256, 2 * size_t(max_chunks + 1) * sizeof(int), st>>>(mask, T, E, K, block, has_shared, ntok, tiled,
                                                                      bits, count, start, bpre, units_gu, units_dn,
                                                                      tunits_gu, tunits_dn, n_units, g_gu, g_dn,
                                                                      tstart);

@@ -393,11 +393,8 @@ __global__ void __launch_bounds__(NTHREADS) tiled_gemm(GemmArgs a) {
         if (rb0 >= rb1) continue;
 #ifdef LLMOE_TILED_TRACE
         TRACE_AT(u, 0);
-        {
-            unsigned hw;
-            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
-            trace_put(4 * u + 3, (unsigned long long)(c | (it.expert << 20)) | ((unsigned long long)hw << 32));
-        }
+        trace_put(4 * u + 3, (unsigned long long)((c & 0xFFFF) | ((rb1 - rb0) << 16) | (((it.ntok + 15) >> 4) << 22) |
+                                                  (bits << 25)) | ((unsigned long long)it.expert << 32));
 #endif
         // token tiles actually present (a chunk has <= 64 slots; absent tiles are not computed)
         const int nt = (it.ntok + 15) >> 4;
@@ -414,11 +411,16 @@ __global__ void __launch_bounds__(NTHREADS) tiled_gemm(GemmArgs a) {
             else if (bits == 3) tiled_body<3, MODE, 3>(a, it, lds, rb0, rb1, u);
             else if (bits == 4) tiled_body<4, MODE, 3>(a, it, lds, rb0, rb1, u);
             else tiled_body<8, MODE, 3>(a, it, lds, rb0, rb1, u);
-        } else {
+        } else if (nt == 2) {
             if (bits == 2) tiled_body<2, MODE, 2>(a, it, lds, rb0, rb1, u);
             else if (bits == 3) tiled_body<3, MODE, 2>(a, it, lds, rb0, rb1, u);
             else if (bits == 4) tiled_body<4, MODE, 2>(a, it, lds, rb0, rb1, u);
             else tiled_body<8, MODE, 2>(a, it, lds, rb0, rb1, u);
+        } else {
+            if (bits == 2) tiled_body<2, MODE, 1>(a, it, lds, rb0, rb1, u);
+            else if (bits == 3) tiled_body<3, MODE, 1>(a, it, lds, rb0, rb1, u);
+            else if (bits == 4) tiled_body<4, MODE, 1>(a, it, lds, rb0, rb1, u);
+            else tiled_body<8, MODE, 1>(a, it, lds, rb0, rb1, u);
         }
 #endif
         __syncthreads();   // the next chunk re-stages the activations
