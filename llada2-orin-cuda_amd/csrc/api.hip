@@ -300,7 +300,7 @@ int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t bl
     ALLOC(L->units_dn, L->items_cap * MAX_UNITS_PER_ITEM);
     ALLOC(L->n_units, 4);
     L->chunks_cap = E + (Tm * K + TILED_NTOK - 1) / TILED_NTOK + (Tm + TILED_NTOK - 1) / TILED_NTOK + 2;
-    if (2 * (L->chunks_cap + 1) * sizeof(int) > 65536)
+    if ((5 * L->chunks_cap + 2) * sizeof(uint32_t) > 65536)
         return bail(fail(LLMOE_EINVAL, "max_tokens = %d: more tiled chunks than the planner holds", int(Tm)));
     ALLOC(L->tunits_gu, L->chunks_cap);
     ALLOC(L->tunits_dn, L->chunks_cap);

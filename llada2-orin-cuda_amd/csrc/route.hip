@@ -186,18 +186,6 @@ __device__ void emit_shared_units(int E, int T, int K, int ntok, int bits, Item*
     }
 }
 
-// tiled chunks of expert e (c slots from slot st): tiled_per(c) slots each, the last one shorter; Item.rb is
-// filled in with the chunk's position once the whole list is written
-__device__ void emit_tiled_units(int e, int c, int st, int base, Item* tunits_gu) {
-    const int nch = tiled_chunks(c), per = tiled_per(c);
-    for (int j = 0; j < nch; ++j) tunits_gu[base + j] = Item{e, st + j * per, min(per, c - j * per), 0};
-}
-
-// the shared expert's tiled chunks (all T tokens, slots T K + t), the first of the tiled list
-__device__ void emit_shared_tiled_units(int T, int E, int K, Item* tunits_gu) {
-    const int nch = tiled_chunks(T), per = tiled_per(T);
-    for (int j = threadIdx.x; j < nch; j += blockDim.x) tunits_gu[j] = Item{E, T * K + j * per, min(per, T - j * per), 0};
-}
 
 // Cost of one row-block task of a chunk with nt 16-slot tiles, in 50 ns units: a per-row-block part (code
 // unpacking, the weight stream) plus a per-tile part (MFMAs and the fp32 epilogue), as measured on MI355X for
@@ -206,24 +194,19 @@ __device__ __forceinline__ int rb_cost(int bits, int nt, bool down) {
     if (down) return bits == 8 ? 42 + 10 * nt : bits == 3 ? 42 + 21 * nt : bits == 4 ? 48 + 20 * nt : 36 + 20 * nt;
     return bits == 8 ? 64 + 35 * nt : bits == 3 ? 134 + 66 * nt : bits == 4 ? 78 + 72 * nt : 70 + 70 * nt;
 }
-__device__ __forceinline__ int chunk_cost(const Item& it, const int8_t* bits, bool down) {
-    const int b = bits[it.expert];
-    return tiled_row_blocks(down, b) * rb_cost(b, (it.ntok + 15) >> 4, down);
+// the chunk's row-block task cost and row-block count of both GEMMs, packed (cost << 8 | count) for the planner
+__device__ __forceinline__ void chunk_tasks(int bits, int ntok, uint32_t* gu, uint32_t* dn) {
+    const int nt = (ntok + 15) >> 4;
+    *gu = uint32_t(rb_cost(bits, nt, false) << 8) | uint32_t(tiled_row_blocks(false, bits));
+    *dn = uint32_t(rb_cost(bits, nt, true) << 8) | uint32_t(tiled_row_blocks(true, bits));
 }
 
-// first row-block task at or after position lo of the chunk list (positions pre[0 .. n], pre[n] = total)
-__device__ int first_task(const int* pre, int n, int lo, const Item* chunks, const int8_t* bits, bool down) {
-    if (lo >= pre[n]) return n;
-    int a = 0, b = n;                 // pre[a] <= lo < pre[b]
-    while (b - a > 1) {
-        const int m = (a + b) >> 1;
-        if (pre[m] <= lo) a = m;
-        else b = m;
-    }
-    const int nrb = tiled_row_blocks(down, bits[chunks[a].expert]);
-    const int span = (pre[a + 1] - pre[a]) / nrb;
-    const int r = (lo - pre[a] + span - 1) / span;
-    return r >= nrb ? a + 1 : (a | (r << TASK_RB_SHIFT));
+// floor(x / d) for 0 <= x < 2^53, d > 0: a double quotient corrected by integer products
+__device__ __forceinline__ long long floor_div(long long x, long long d) {
+    long long q = (long long)(double(x) / double(d));
+    while (q > 0 && q * d > x) --q;
+    while ((q + 1) * d <= x) ++q;
+    return q;
 }
 
 struct DispatchOut {         // written by the single-block fused route (decode): the plan + place results
@@ -404,6 +387,14 @@ struct DecodeState {
 };
 
 // Slots and work units of the decode step (engine/ops.cu:333-370), one workgroup of 256 threads.
+#ifdef LLMOE_TILED_TRACE
+// timing builds only: s_memrealtime at the planner's phase boundaries
+__device__ unsigned long long g_plan_trace[16];
+#define PLAN_TRACE(k) if (threadIdx.x == 0) g_plan_trace[k] = __builtin_amdgcn_s_memrealtime()
+#else
+#define PLAN_TRACE(k) ((void)0)
+#endif
+
 // Slots: expert-major, token-ascending; shared slots T K + t. Units: items of 16 slots split into row blocks by
 // code width, heaviest first (the shared expert, then 8 / 4 / 3 / 2-bit experts).
 __global__ void __launch_bounds__(256) dispatch_kernel(int T, int E, int K, const int* __restrict__ topk,
@@ -640,21 +631,38 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
                                                    Item* __restrict__ units_gu, Item* __restrict__ units_dn,
                                                    Item* __restrict__ tunits_gu, Item* __restrict__ tunits_dn,
                                                    int* __restrict__ n_units, int g_gu, int g_dn,
-                                                   int* __restrict__ tstart) {
+                                                   int* __restrict__ tstart, int max_chunks) {
     constexpr int NBR = 64;                    // token masks of the first NBR blocks stay in registers
-    extern __shared__ int pre[];               // chunk positions [2][n_chunks + 1] (gate_up, down)
+    // chunk tables (max_chunks entries): row-block tasks of both GEMMs, then their positions [n_chunks + 1]
+    extern __shared__ uint32_t plan_lds[];
+    uint32_t* task_gu = plan_lds;
+    uint32_t* task_dn = task_gu + max_chunks;
+    int* pre_gu = reinterpret_cast<int*>(task_dn + max_chunks);
+    int* pre_dn = pre_gu + max_chunks + 1;
+    int* owner = pre_dn + max_chunks + 1;      // expert of each chunk
     __shared__ int wt_i[4], wt_c[4];
     __shared__ uint64_t wt[4][4];
     __shared__ uint64_t tot[4];
+    __shared__ int first_l[MAXE + 1], cnt_l[MAXE + 1], st_l[MAXE + 1], bits_l[MAXE + 1];
     const int e = threadIdx.x, nb = (T + block - 1) / block, lane = e & 63, w = e >> 6;
+    PLAN_TRACE(0);
+    // token masks: unconditional loads at clamped indices, so that each batch is issued back to back
+    const int ec = min(e, E - 1);
     uint32_t mv[NBR];
 #pragma unroll
-    for (int j = 0; j < NBR; ++j) mv[j] = e < E && j < nb ? mask[size_t(j) * E + e] : 0u;   // one batch of loads
+    for (int j = 0; j < NBR; ++j) mv[j] = mask[size_t(min(j, nb - 1)) * E + ec];
     int c = 0;
 #pragma unroll
-    for (int j = 0; j < NBR; ++j) c += __popc(mv[j]);
-    if (e < E)
-        for (int b = NBR; b < nb; ++b) c += __popc(mask[size_t(b) * E + e]);
+    for (int j = 0; j < NBR; ++j) c += j < nb ? __popc(mv[j]) : 0;
+    for (int b0 = NBR; b0 < nb; b0 += 16) {
+        uint32_t m2[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) m2[j] = mask[size_t(min(b0 + j, nb - 1)) * E + ec];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) c += b0 + j < nb ? __popc(m2[j]) : 0;
+    }
+    if (e >= E) c = 0;
+    PLAN_TRACE(1);
     const bool big = e < E && tiled && c > 0;
     const bool sbig = has_shared && tiled;
     const int nsch = sbig ? tiled_chunks(T) : 0;
@@ -727,32 +735,63 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
                 bpre[size_t(j) * E + e] = run;
                 run += __popc(mv[j]);
             }
-        for (int b = NBR; b < nb; ++b) {
-            bpre[size_t(b) * E + e] = run;
-            run += __popc(mask[size_t(b) * E + e]);
+        for (int b0 = NBR; b0 < nb; b0 += 16) {
+            uint32_t m2[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) m2[j] = mask[size_t(min(b0 + j, nb - 1)) * E + e];
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (b0 + j < nb) {
+                    bpre[size_t(b0 + j) * E + e] = run;
+                    run += __popc(m2[j]);
+                }
         }
-        if (big) emit_tiled_units(e, c, st, ot, tunits_gu);
-        else emit_units(e, c, st, ntok, bw, og, od, units_gu, units_dn);
+        if (big) {   // the chunks are written below, one thread per chunk
+            first_l[e] = ot;
+            cnt_l[e] = c;
+            st_l[e] = st;
+            bits_l[e] = bw;
+            for (int j = 0; j < nch; ++j) owner[ot + j] = e;
+        } else {
+            emit_units(e, c, st, ntok, bw, og, od, units_gu, units_dn);
+        }
     }
     if (ns) emit_shared_units(E, T, K, ntok, sbits, units_gu, units_dn);
-    if (sbig) emit_shared_tiled_units(T, E, K, tunits_gu);
+    if (sbig) {
+        if (e == 0) {
+            first_l[E] = 0;
+            cnt_l[E] = T;
+            st_l[E] = T * K;
+            bits_l[E] = sbits;
+        }
+        for (int j = e; j < nsch; j += blockDim.x) owner[j] = E;
+    }
     if (e == 0) {
         n_units[0] = bg;
         n_units[1] = bd;
         n_units[2] = bt;
         n_units[3] = bt;
     }
+    PLAN_TRACE(2);
     if (!tiled) return;
-    // chunk positions of both GEMMs: scans of the chunk costs over the written list (each thread a run of
-    // consecutive chunks)
-    __threadfence_block();
+    // the tiled chunks: tiled_per(c) slots of an expert's c each, the last one shorter (Item.rb unused)
     __syncthreads();
-    const int n = bt, per = (n + blockDim.x - 1) / blockDim.x, j0 = min(n, e * per), j1 = min(n, j0 + per);
+    const int n = bt;
+    for (int j = e; j < n; j += blockDim.x) {
+        const int x = owner[j], cx = cnt_l[x], pc = tiled_per(cx), jj = j - first_l[x];
+        const Item it{x, st_l[x] + jj * pc, min(pc, cx - jj * pc), 0};
+        tunits_gu[j] = it;
+        tunits_dn[j] = it;
+        chunk_tasks(bits_l[x], it.ntok, &task_gu[j], &task_dn[j]);
+    }
+    // chunk positions of both GEMMs: scans of the chunk costs (each thread a run of consecutive chunks)
+    __syncthreads();
+    const int per = (n + blockDim.x - 1) / blockDim.x, j0 = min(n, e * per), j1 = min(n, j0 + per);
+    auto cost = [](uint32_t t) { return int(t >> 8) * int(t & 255u); };
     int run0 = 0, run1 = 0;
     for (int j = j0; j < j1; ++j) {
-        const Item it = tunits_gu[j];
-        run0 += chunk_cost(it, bits, false);
-        run1 += chunk_cost(it, bits, true);
+        run0 += cost(task_gu[j]);
+        run1 += cost(task_dn[j]);
     }
     int inc0 = run0, inc1 = run1;
 #pragma unroll
@@ -772,32 +811,45 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
         inc0 += wt_i[i];
         inc1 += wt_c[i];
     }
-    int* pre_dn = pre + n + 1;
     run0 = inc0 - run0;
     run1 = inc1 - run1;
     for (int j = j0; j < j1; ++j) {
-        Item it = tunits_gu[j];
-        pre[j] = run0;
+        pre_gu[j] = run0;
         pre_dn[j] = run1;
-        run0 += chunk_cost(it, bits, false);
-        run1 += chunk_cost(it, bits, true);
-        it.rb = pre[j];
-        tunits_gu[j] = it;
-        it.rb = pre_dn[j];
-        tunits_dn[j] = it;
+        run0 += cost(task_gu[j]);
+        run1 += cost(task_dn[j]);
     }
     if (e == blockDim.x - 1) {
-        pre[n] = inc0;
+        pre_gu[n] = inc0;
         pre_dn[n] = inc1;
     }
     __syncthreads();
-    for (int q = e; q <= g_gu + g_dn + 1; q += blockDim.x) {
-        const bool down = q > g_gu;
-        const int wg = down ? q - g_gu - 1 : q, G = down ? g_dn : g_gu;
-        const int* P = down ? pre_dn : pre;
-        const long long total = P[n], x = (long long)(wg) * total;
-        tstart[q] = first_task(P, n, int(x / G + (x % G != 0)), tunits_gu, bits, down);
+    PLAN_TRACE(3);
+    // work partition: chunk j hands workgroup w (lo_w = ceil(w C / G) in [pre_j, pre_j+1)) its first task
+    for (int m = 0; m < 2; ++m) {
+        const int G = m ? g_dn : g_gu;
+        const int* P = m ? pre_dn : pre_gu;
+        const uint32_t* task = m ? task_dn : task_gu;
+        int* ts = tstart + (m ? g_gu + 1 : 0);
+        const long long C = P[n];
+        if (e == 0) ts[G] = n;
+        if (C == 0) {
+            for (int q = e; q < G; q += blockDim.x) ts[q] = n;
+            continue;
+        }
+        // workgroups past the last task start (lo_w >= C, possible when C < G) get none
+        for (long long q = floor_div((C - 1) * G, C) + 1 + e; q < G; q += blockDim.x) ts[q] = n;
+        for (int j = e; j < n; j += blockDim.x) {
+            const int p0 = P[j], p1 = P[j + 1], nrb = int(task[j] & 255u), span = int(task[j] >> 8);
+            for (long long q = p0 == 0 ? 0 : floor_div((long long)(p0 - 1) * G, C) + 1; q < G; ++q) {
+                const long long lo = floor_div(q * C + G - 1, G);
+                if (lo >= p1) break;
+                const int r = int((lo - p0 + span - 1) / span);
+                ts[q] = r >= nrb ? j + 1 : (j | (r << TASK_RB_SHIFT));
+            }
+        }
     }
+    PLAN_TRACE(4);
 }
 
 // Place every (token, k) pair in its slot; tok_slots[t, K] = the shared slot (or -1). grid nb, 256 threads.
@@ -878,10 +930,10 @@ hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int
                        const int8_t* bits, int32_t* count, int32_t* start, int32_t* bpre, Item* units_gu,
                        Item* units_dn, Item* tunits_gu, Item* tunits_dn, int* n_units, int g_gu, int g_dn,
                        int* tstart, int max_chunks, hipStream_t st) {
-    plan_kernel<<<1, 256, 2 * size_t(max_chunks + 1) * sizeof(int), st>>>(mask, T, E, K, block, has_shared, ntok, tiled,
-                                                                     bits, count, start, bpre, units_gu, units_dn,
-                                                                     tunits_gu, tunits_dn, n_units, g_gu, g_dn,
-                                                                     tstart);
+    const size_t lds = (5 * size_t(max_chunks) + 2) * sizeof(uint32_t);
+    plan_kernel<<<1, 256, lds, st>>>(mask, T, E, K, block, has_shared, ntok, tiled, bits, count, start, bpre,
+                                     units_gu, units_dn, tunits_gu, tunits_dn, n_units, g_gu, g_dn, tstart,
+                                     max_chunks);
     return hipGetLastError();
 }
 
@@ -895,3 +947,9 @@ hipError_t launch_place(const int32_t* topk, const float* topw, const uint32_t* 
 }
 
 }  // namespace llmoe
+
+#ifdef LLMOE_TILED_TRACE
+extern "C" int llmoe_plan_trace(void* host) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(llmoe::g_plan_trace), 16 * 8) == hipSuccess ? 0 : -1;
+}
+#endif
