@@ -123,7 +123,9 @@ __host__ __device__ constexpr int b_bytes(int ntok, int K) { return ntok * (K + 
 template <int MODE>
 __host__ __device__ constexpr int meta_bytes() { return WAVES * Geo<MODE>::SPW_MAX * Geo<MODE>::NSB * META_SB; }
 template <int MODE, int NT>
-__host__ __device__ constexpr int lds_bytes() { return b_bytes(16 * NT, Geo<MODE>::NSB * SB_K) + meta_bytes<MODE>(); }
+__host__ __device__ constexpr int lds_bytes() {
+    return b_bytes(16 * NT, Geo<MODE>::NSB * SB_K) + meta_bytes<MODE>() + 16 * NT * 4;   // + the B row table
+}
 
 template <int BITS, int MODE, int NT>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uint8_t* lds, int row_block) {
@@ -169,30 +171,30 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
     int* bsum = reinterpret_cast<int*>(bs + G * NTOK);
     const int ntok = it.ntok;
     {
-        // B rows: NTOK * K / 16 chunks of 16 bytes over 256 threads; all loads issued before the LDS stores
+        // B rows through a row table in LDS (one round of slot_token loads), then NTOK * K / 16 chunks of 16
+        // bytes over 256 threads at clamped rows, all issued before the LDS stores
+        int* rowtab = reinterpret_cast<int*>(meta_lds + meta_bytes<MODE>());
+        if (threadIdx.x < NTOK) {
+            const int slot = it.slot0 + min(int(threadIdx.x), ntok - 1);
+            rowtab[threadIdx.x] = a.slot_token ? a.slot_token[slot] : slot;
+        }
+        __syncthreads();
         constexpr int CH = K / 16, PER = (NTOK * CH + WAVES * 64 - 1) / (WAVES * 64);
         u4 v[PER];
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int idx = threadIdx.x + i * WAVES * 64, n = idx / CH, c16 = idx % CH;
-            if (n < ntok) {
-                const int slot = it.slot0 + n;
-                const size_t row = a.slot_token ? size_t(a.slot_token[slot]) : size_t(slot);
-                v[i] = *reinterpret_cast<const u4*>(a.xq + row * K + 16 * c16);
-            }
+            const int idx = threadIdx.x + i * WAVES * 64, c16 = idx % CH;
+            v[i] = *reinterpret_cast<const u4*>(a.xq + size_t(rowtab[min(idx / CH, NTOK - 1)]) * K + 16 * c16);
         }
         constexpr int PG = (NTOK * G + WAVES * 64 - 1) / (WAVES * 64);
         float sv[PG];
         int qv[PG];
 #pragma unroll
         for (int i = 0; i < PG; ++i) {
-            const int idx = threadIdx.x + i * WAVES * 64, n = idx / G, g = idx % G;
-            if (n < ntok) {
-                const int slot = it.slot0 + n;
-                const size_t row = a.slot_token ? size_t(a.slot_token[slot]) : size_t(slot);
-                sv[i] = a.xs ? a.xs[row * G + g] : 0.0f;
-                qv[i] = a.xsum[row * G + g];
-            }
+            const int idx = threadIdx.x + i * WAVES * 64, g = idx % G;
+            const size_t row = size_t(rowtab[min(idx / G, NTOK - 1)]);
+            sv[i] = a.xs ? a.xs[row * G + g] : 0.0f;
+            qv[i] = a.xsum[row * G + g];
         }
         // rows n >= ntok are zero: the MFMA columns of absent tokens then compute zeros, branch-free
 #pragma unroll
