@@ -239,54 +239,103 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
         const u4 ms0 = *reinterpret_cast<const u4*>(mp + 32 * q);
         const u4 ms1 = *reinterpret_cast<const u4*>(mp + 32 * q + 16);
         const u4 zw4 = *reinterpret_cast<const u4*>(mp + 128 + 16 * q);
+        if constexpr (!Geo<MODE>::PRODUCTS && NT == 1) {
+            // layer GEMMs (one token tile): software-pipelined over the 4 tiles, the MFMAs of tile tau issued
+            // before the fp32 epilogue of tile tau - 1, so the MFMA latency overlaps vector work
+            v4i Cp;
+            float xsp = 0.0f;
+            uint32_t swpp[2] = {0u, 0u};
+            static_for<0, 5>([&](auto tc) {
+                constexpr int tau = decltype(tc)::value;
+                v4i Cc;
+                float xsc = 0.0f;
+                uint32_t swc[2] = {0u, 0u};
+                if constexpr (tau < 4) {
+                    constexpr int g = sb * 4 + tau;
+                    uint32_t Dw[8];
+                    unpack_tile<BITS>(cur, tau, Dw);
+                    const v4i A0 = {int(Dw[0]), int(Dw[1]), int(Dw[2]), int(Dw[3])};
+                    const v4i A1 = {int(Dw[4]), int(Dw[5]), int(Dw[6]), int(Dw[7])};
+                    const uint32_t zw = zw4[tau];
+                    const u4& sv = tau < 2 ? ms0 : ms1;
+                    swc[0] = wsel(sv, (tau & 1) * 2);
+                    swc[1] = wsel(sv, (tau & 1) * 2 + 1);
+                    int zz[4];
 #pragma unroll
-        for (int tau = 0; tau < 4; ++tau) {
-            const int g = sb * 4 + tau;
-            uint32_t Dw[8];
-            unpack_tile<BITS>(cur, tau, Dw);
-            const v4i A0 = {int(Dw[0]), int(Dw[1]), int(Dw[2]), int(Dw[3])};
-            const v4i A1 = {int(Dw[4]), int(Dw[5]), int(Dw[6]), int(Dw[7])};
-            const uint32_t zw = zw4[tau];
-            const u4& sv = tau < 2 ? ms0 : ms1;
-            const uint32_t s01 = wsel(sv, (tau & 1) * 2), s23 = wsel(sv, (tau & 1) * 2 + 1);
-            const uint32_t swp[2] = {s01, s23};   // fp16 scale pairs (rows 4q + 0, 1 | 2, 3)
-            int zz[4];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) zz[v] = int((zw >> (8 * v)) & 0xFFu) - ZOFF;
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const int n = nt * 16 + col;
-                const int8_t* br = bq + n * LDQ + g * GROUP + 16 * q;
-                const v4i B0 = *reinterpret_cast<const v4i*>(br);
-                const v4i B1 = *reinterpret_cast<const v4i*>(br + 64);
-                const float xsn = bs[g * NTOK + n];
-                const int nxsum = bsum[g * NTOK + n];
-                v4i C = {__mul24(zz[0], nxsum), __mul24(zz[1], nxsum), __mul24(zz[2], nxsum), __mul24(zz[3], nxsum)};
-                C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, C, 0, 0, 0);
-                C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, C, 0, 0, 0);
-                if constexpr (Geo<MODE>::PRODUCTS) {
-                    if (n < ntok) {
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) {
-                            const int d = 4 * q + v;
-                            const int prow = 16 * strip + (MODE == GEMM_PRODUCTS_GATE_UP ? gu_packlib_row(d) : d);
-                            a.P[(size_t(it.slot0 + n) * a.R + prow) * G + g] = C[v];
-                        }
-                    }
-                } else {
+                    for (int v = 0; v < 4; ++v) zz[v] = int((zw >> (8 * v)) & 0xFFu) - ZOFF;
+                    const int8_t* br = bq + col * LDQ + g * GROUP + 16 * q;
+                    const v4i B0 = *reinterpret_cast<const v4i*>(br);
+                    const v4i B1 = *reinterpret_cast<const v4i*>(br + 64);
+                    xsc = bs[g * NTOK + col];
+                    const int nxsum = bsum[g * NTOK + col];
+                    Cc = v4i{__mul24(zz[0], nxsum), __mul24(zz[1], nxsum), __mul24(zz[2], nxsum), __mul24(zz[3], nxsum)};
+                    Cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, Cc, 0, 0, 0);
+                    Cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, Cc, 0, 0, 0);
+                }
+                if constexpr (tau > 0) {
 #pragma unroll
                     for (int v = 0; v < 4; ++v)
-                        acc[nt][v] = __builtin_fmaf(mul_f16_f32(swp[v >> 1], v & 1, xsn), float(C[v]), acc[nt][v]);
+                        acc[0][v] = __builtin_fmaf(mul_f16_f32(swpp[v >> 1], v & 1, xsp), float(Cp[v]), acc[0][v]);
+                    asm volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[0][2]), "+v"(acc[0][3]));
                 }
+                if constexpr (tau < 4) {
+                    Cp = Cc;
+                    xsp = xsc;
+                    swpp[0] = swc[0];
+                    swpp[1] = swc[1];
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        } else {
+    #pragma unroll
+            for (int tau = 0; tau < 4; ++tau) {
+                const int g = sb * 4 + tau;
+                uint32_t Dw[8];
+                unpack_tile<BITS>(cur, tau, Dw);
+                const v4i A0 = {int(Dw[0]), int(Dw[1]), int(Dw[2]), int(Dw[3])};
+                const v4i A1 = {int(Dw[4]), int(Dw[5]), int(Dw[6]), int(Dw[7])};
+                const uint32_t zw = zw4[tau];
+                const u4& sv = tau < 2 ? ms0 : ms1;
+                const uint32_t s01 = wsel(sv, (tau & 1) * 2), s23 = wsel(sv, (tau & 1) * 2 + 1);
+                const uint32_t swp[2] = {s01, s23};   // fp16 scale pairs (rows 4q + 0, 1 | 2, 3)
+                int zz[4];
+    #pragma unroll
+                for (int v = 0; v < 4; ++v) zz[v] = int((zw >> (8 * v)) & 0xFFu) - ZOFF;
+    #pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const int n = nt * 16 + col;
+                    const int8_t* br = bq + n * LDQ + g * GROUP + 16 * q;
+                    const v4i B0 = *reinterpret_cast<const v4i*>(br);
+                    const v4i B1 = *reinterpret_cast<const v4i*>(br + 64);
+                    const float xsn = bs[g * NTOK + n];
+                    const int nxsum = bsum[g * NTOK + n];
+                    v4i C = {__mul24(zz[0], nxsum), __mul24(zz[1], nxsum), __mul24(zz[2], nxsum), __mul24(zz[3], nxsum)};
+                    C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, C, 0, 0, 0);
+                    C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, C, 0, 0, 0);
+                    if constexpr (Geo<MODE>::PRODUCTS) {
+                        if (n < ntok) {
+    #pragma unroll
+                            for (int v = 0; v < 4; ++v) {
+                                const int d = 4 * q + v;
+                                const int prow = 16 * strip + (MODE == GEMM_PRODUCTS_GATE_UP ? gu_packlib_row(d) : d);
+                                a.P[(size_t(it.slot0 + n) * a.R + prow) * G + g] = C[v];
+                            }
+                        }
+                    } else {
+    #pragma unroll
+                        for (int v = 0; v < 4; ++v)
+                            acc[nt][v] = __builtin_fmaf(mul_f16_f32(swp[v >> 1], v & 1, xsn), float(C[v]), acc[nt][v]);
+                    }
+                }
+                // one tile at a time: the accumulators are materialised here, otherwise the compiler defers each
+                // tile's fp32 accumulation (a serial fma chain) to the strip end and keeps every tile's results live
+                if constexpr (!Geo<MODE>::PRODUCTS) {
+    #pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+                        asm volatile("" : "+v"(acc[nt][0]), "+v"(acc[nt][1]), "+v"(acc[nt][2]), "+v"(acc[nt][3]));
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            // one tile at a time: the accumulators are materialised here, otherwise the compiler defers each
-            // tile's fp32 accumulation (a serial fma chain) to the strip end and keeps every tile's results live
-            if constexpr (!Geo<MODE>::PRODUCTS) {
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
-                    asm volatile("" : "+v"(acc[nt][0]), "+v"(acc[nt][1]), "+v"(acc[nt][2]), "+v"(acc[nt][3]));
-            }
-            __builtin_amdgcn_sched_barrier(0);
         }
         if constexpr (!Geo<MODE>::PRODUCTS && sb == NSB - 1) {   // strip done: fused epilogue
 #pragma unroll
