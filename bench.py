@@ -250,6 +250,26 @@ def prefill_config(llmoe, synth, torch, name, T, mix, shared, pool, logits_kind,
             "int8_mfma_frac_peak": 2 * slots * 3 * I * H / t_w / 1e12 / PEAK_INT8_TOPS}
 
 
+def dense_config(llmoe, synth, torch, R, bits, T, steps, warmup, nmat=40):
+    """Dense W.A8 projection (llmoe_dense_forward, the qkv shape of the reference engine: [3072, 2048]): a step is
+    one projection of T tokens' A8 rows; the steps cycle through nmat matrices (> 256 MB) so the weights stream
+    from HBM."""
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(77)
+    Ds = [llmoe.Dense(synth.random_matrix(rng, R, H, bits), R, bits, max_tokens=T) for _ in range(nmat)]
+    xq, xs, xsum = llmoe.quantize_a8(torch.from_numpy(synth.make_x(9, T)).to(dev))
+    y = torch.empty((T, R), dtype=torch.float32, device=dev)
+    dt = time_steps(lambda i: Ds[i % nmat].forward(xq, xs, xsum, out=y), steps, warmup)
+    for D in Ds:
+        D.close()
+    t = dt / steps
+    wb = synth.matrix_bytes(R, H, bits)
+    return {"workload": f"dense W{bits}A8 projection [{R} x {H}] (qkv shape), {T} tokens", "tokens": T,
+            "ms_per_step": t * 1e3, "tokens_per_s": T / t, "weight_bytes": wb, "weight_stream_GBps": wb / t / 1e9,
+            "weight_stream_frac_peak": wb / t / 1e9 / PEAK_HBM_GBS, "int8_TOPS": 2 * T * R * H / t / 1e12,
+            "int8_mfma_frac_peak": 2 * T * R * H / t / 1e12 / PEAK_INT8_TOPS}
+
+
 def cpu_baseline(L, x_np, pool, seconds):
     import oracle
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
@@ -316,6 +336,9 @@ def main():
                                       48, None, max(2, args.steps // 10), 2, outliers=0.01))
         log("[bench] config 3")
         configs.append(stack_config(llmoe, synth, torch, max(1, args.steps // 20), max(1, args.warmup // 10)))
+        for T in (32, 2048):
+            log(f"[bench] dense projection, {T} tokens")
+            configs.append(dense_config(llmoe, synth, torch, 3072, 8, T, max(5, args.steps // 4), 5))
         for bits in (2, 4, 8):
             for kind in ("uniform", "skewed"):
                 log(f"[bench] config 4: {bits}-bit {kind}")

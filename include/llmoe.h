@@ -179,6 +179,22 @@ int llmoe_layer_load(const char* model_dir, int layer, int max_tokens, llmoe_lay
 /* The residual-rotation signs (small.bin "signs", fp32 [n], Q = diag(signs) H / sqrt(n)) into host memory. */
 int llmoe_model_signs(const char* model_dir, float* signs, int n);
 
+/* Dense W.A8 projection (engine/engine.cu:380-383, :425, :434: qkv, the attention output and the lm_head run
+ * through the expert GEMM as one "expert" holding every token; KAT engine/tests/gen_dense_case.py). One [rows, k]
+ * matrix of b-bit codes in packlib "i8" (quant/packlib.py), rows in packlib order; k = 2048, rows a multiple of
+ * 256, bits 2 / 3 / 4 / 8. The blob is read once, relaid out on the device and not kept. */
+typedef struct llmoe_dense llmoe_dense;
+int llmoe_dense_create(int rows, int k, int bits, const uint8_t* blob, size_t blob_bytes, int max_tokens,
+                       llmoe_dense** out);
+int llmoe_dense_destroy(llmoe_dense* dense);
+
+/* y[t, r] = sum over the 16 groups g (ascending) of the fma chain of scale_w[r, g] * xs[t, g] and the exact int32
+ * group product (the expert GEMMs' epilogue), for the T <= max_tokens A8 rows (xq int8 [T, 2048], xs fp32 [T, 16],
+ * xsum int32 [T, 16], the llmoe_quantize_a8 layout); accumulate != 0: y += that (the residual add of
+ * engine/engine.cu:434). y fp32 [T, rows] on the device; asynchronous on `stream`. */
+int llmoe_dense_forward(llmoe_dense* dense, const int8_t* xq, const float* xs, const int32_t* xsum, int T, float* y,
+                        int accumulate, llmoe_stream stream);
+
 /* Message of the calling thread's last error ("" if none). */
 const char* llmoe_last_error(void);
 

@@ -37,20 +37,27 @@ int fail(int code, const char* fmt, ...) {
                                           __FILE__, __LINE__);                                             \
     } while (0)
 
-int tile_wbytes(int bits) { return bits == 8 ? 2048 : bits == 4 ? 1024 : bits == 3 ? 768 : bits == 2 ? 512 : -1; }
-size_t packlib_matrix_bytes(int R, int K, int bits) {
-    return size_t(R / 16) * size_t(K / GROUP) * size_t(tile_wbytes(bits) + 48);
-}
-
 hipError_t g_setup = hipErrorNotInitialized;
 bool g_setup_done = false;
 
 }  // namespace
 
 namespace llmoe {
+int tile_wbytes(int bits) { return bits == 8 ? 2048 : bits == 4 ? 1024 : bits == 3 ? 768 : bits == 2 ? 512 : -1; }
+size_t packlib_matrix_bytes(int R, int K, int bits) {
+    return size_t(R / 16) * size_t(K / GROUP) * size_t(tile_wbytes(bits) + 48);
+}
 int set_error(int code, const char* msg) {
     g_err = msg;
     return code;
+}
+int ensure_gemm_setup() {
+    if (!g_setup_done) {
+        g_setup = gemm_setup();
+        if (g_setup == hipSuccess) g_setup = tiled_setup();
+        g_setup_done = true;
+    }
+    return g_setup == hipSuccess ? LLMOE_OK : fail(LLMOE_EHIP, "gemm_setup: %s", hipGetErrorString(g_setup));
 }
 }  // namespace llmoe
 
@@ -211,12 +218,7 @@ int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t bl
         if (gu_off[e] + gb > blob_bytes || d_off[e] + db > blob_bytes)
             return fail(LLMOE_EINVAL, "expert %d: matrix beyond the blob (%zu bytes)", e, blob_bytes);
     }
-    if (!g_setup_done) {
-        g_setup = gemm_setup();
-        if (g_setup == hipSuccess) g_setup = tiled_setup();
-        g_setup_done = true;
-    }
-    if (g_setup != hipSuccess) return fail(LLMOE_EHIP, "gemm_setup: %s", hipGetErrorString(g_setup));
+    if (int rc = llmoe::ensure_gemm_setup()) return rc;
 
     llmoe_layer* L = new (std::nothrow) llmoe_layer();
     if (!L) return fail(LLMOE_ENOMEM, "host allocation");

@@ -343,7 +343,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
                 const int n = nt * 16 + col;
                 if (n < ntok) {
                     const int slot = it.slot0 + n;
-                    if constexpr (MODE == GEMM_GATE_UP) {
+                    if constexpr (MODE == GEMM_DENSE) {
+                        float4* yp = reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q);
+                        float4 y = make_float4(acc[nt][0], acc[nt][1], acc[nt][2], acc[nt][3]);
+                        if (a.accumulate) {
+                            const float4 o = *yp;
+                            y = make_float4(o.x + y.x, o.y + y.y, o.z + y.z, o.w + y.w);
+                        }
+                        *yp = y;
+                    } else if constexpr (MODE == GEMM_GATE_UP) {
                         // lane quad q holds rows gate 8 strip + 2q, up (same), gate + 1, up + 1
                         const uint32_t z0 = f32_to_f16_bits(silu_f32(acc[nt][0]) * acc[nt][1]);
                         const uint32_t z1 = f32_to_f16_bits(silu_f32(acc[nt][2]) * acc[nt][3]);
@@ -412,6 +420,7 @@ hipError_t gemm_setup() {
     hipError_t e;
     if ((e = set_attr<GEMM_GATE_UP, 1>()) != hipSuccess) return e;
     if ((e = set_attr<GEMM_DOWN, 1>()) != hipSuccess) return e;
+    if ((e = set_attr<GEMM_DENSE, 1>()) != hipSuccess) return e;
     if ((e = set_attr<GEMM_PRODUCTS_GATE_UP, 4>()) != hipSuccess) return e;
     if ((e = set_attr<GEMM_PRODUCTS_DOWN, 4>()) != hipSuccess) return e;
     return hipSuccess;
@@ -422,6 +431,7 @@ hipError_t gemm_setup() {
 hipError_t launch_expert_gemm(int mode, int nt, const GemmArgs& a, int max_items, hipStream_t st) {
     if (mode == GEMM_GATE_UP) return nt == 1 ? launch_t<GEMM_GATE_UP, 1>(a, max_items, st) : hipErrorInvalidValue;
     if (mode == GEMM_DOWN) return nt == 1 ? launch_t<GEMM_DOWN, 1>(a, max_items, st) : hipErrorInvalidValue;
+    if (mode == GEMM_DENSE) return nt == 1 ? launch_t<GEMM_DENSE, 1>(a, max_items, st) : hipErrorInvalidValue;
     if (mode == GEMM_PRODUCTS_GATE_UP) return launch_t<GEMM_PRODUCTS_GATE_UP, 4>(a, max_items, st);
     return launch_t<GEMM_PRODUCTS_DOWN, 4>(a, max_items, st);
 }

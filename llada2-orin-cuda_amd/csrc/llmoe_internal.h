@@ -143,12 +143,19 @@ struct GemmArgs {
     float* Y;                   // down out [slots, R]
     int32_t* P;                 // group-products out [n, R, K/128] (test entry)
     const int* tstart;          // tiled: [G + 1] first task of each workgroup (the work partition above)
+    int accumulate;             // GEMM_DENSE: Y += acc instead of Y = acc
 };
 
-enum GemmMode { GEMM_GATE_UP = 0, GEMM_DOWN = 1, GEMM_PRODUCTS_GATE_UP = 2, GEMM_PRODUCTS_DOWN = 3 };
+// GEMM_DENSE: a plain W.A8 projection [R, 2048] (rows in packlib order), out Y[token, r] = acc (or += acc)
+enum GemmMode { GEMM_GATE_UP = 0, GEMM_DOWN = 1, GEMM_PRODUCTS_GATE_UP = 2, GEMM_PRODUCTS_DOWN = 3, GEMM_DENSE = 4 };
 
 // records msg as the calling thread's last error (llmoe_last_error) and returns code
 int set_error(int code, const char* msg);
+// the GEMM kernels' function attributes, once per process (LLMOE_OK or an error recorded as above)
+int ensure_gemm_setup();
+// packlib "i8" bytes of an [R, K] matrix of b-bit codes (-1 tile bytes: unsupported width)
+int tile_wbytes(int bits);
+size_t packlib_matrix_bytes(int R, int K, int bits);
 
 hipError_t gemm_setup();   // function attributes (dynamic LDS), once per process
 hipError_t launch_expert_gemm(int mode, int nt, const GemmArgs& a, int max_items, hipStream_t st);

@@ -338,7 +338,15 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
             const int n = nt * 16 + col;
             if (n < it.ntok) {
                 const int slot = it.slot0 + n;
-                if constexpr (MODE == GEMM_GATE_UP) {
+                if constexpr (MODE == GEMM_DENSE) {
+                    float4* yp = reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q);
+                    float4 y = make_float4(acc[s][nt][0], acc[s][nt][1], acc[s][nt][2], acc[s][nt][3]);
+                    if (a.accumulate) {
+                        const float4 o = *yp;
+                        y = make_float4(o.x + y.x, o.y + y.y, o.z + y.z, o.w + y.w);
+                    }
+                    *yp = y;
+                } else if constexpr (MODE == GEMM_GATE_UP) {
                     const uint32_t z0 = f32_to_f16_bits(silu_f32(acc[s][nt][0]) * acc[s][nt][1]);
                     const uint32_t z1 = f32_to_f16_bits(silu_f32(acc[s][nt][2]) * acc[s][nt][3]);
                     *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
@@ -389,7 +397,8 @@ __global__ void __launch_bounds__(NTHREADS) tiled_gemm(GemmArgs a) {
     for (int c = c0; c < c1 || (c == c1 && r1 > 0); ++c) {
         const Item it = a.items[c];
         const int bits = a.bits[it.expert];
-        const int rb0 = c == c0 ? r0 : 0, rb1 = c == c1 ? r1 : tiled_row_blocks(MODE == GEMM_DOWN, bits);
+        const int nrb = MODE == GEMM_DENSE ? a.R / (16 * NW * tiled_spw(bits)) : tiled_row_blocks(MODE == GEMM_DOWN, bits);
+        const int rb0 = c == c0 ? r0 : 0, rb1 = c == c1 ? r1 : nrb;
         if (rb0 >= rb1) continue;
 #ifdef LLMOE_TILED_TRACE
         TRACE_AT(u, 0);
@@ -461,14 +470,18 @@ hipError_t launch_t(const GemmArgs& a, hipStream_t st) {
 hipError_t tiled_setup() {
     hipError_t e = hipFuncSetAttribute(kptr<GEMM_GATE_UP>(), hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
     if (e == hipSuccess) e = hipFuncSetAttribute(kptr<GEMM_DOWN>(), hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+    if (e == hipSuccess) e = hipFuncSetAttribute(kptr<GEMM_DENSE>(), hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
     return e;
 }
 
-int tiled_grid(int mode) { return mode == GEMM_DOWN ? grid_t<GEMM_DOWN>() : grid_t<GEMM_GATE_UP>(); }
+int tiled_grid(int mode) {
+    return mode == GEMM_DOWN ? grid_t<GEMM_DOWN>() : mode == GEMM_DENSE ? grid_t<GEMM_DENSE>() : grid_t<GEMM_GATE_UP>();
+}
 
 hipError_t launch_tiled_gemm(int mode, const GemmArgs& a, hipStream_t st) {
     if (mode == GEMM_GATE_UP) return launch_t<GEMM_GATE_UP>(a, st);
     if (mode == GEMM_DOWN) return launch_t<GEMM_DOWN>(a, st);
+    if (mode == GEMM_DENSE) return launch_t<GEMM_DENSE>(a, st);
     return hipErrorInvalidValue;
 }
 

@@ -63,7 +63,8 @@ EXPORTS = [
     "llmoe_layer_create", "llmoe_layer_destroy", "llmoe_quantize_a8", "llmoe_route", "llmoe_dispatch",
     "llmoe_experts", "llmoe_experts_norm", "llmoe_layer_forward", "llmoe_layer_buffers", "llmoe_layer_weight_bytes",
     "llmoe_group_products", "llmoe_layer_set_profiling", "llmoe_layer_stage_ms", "llmoe_layer_time_stage", "llmoe_layers_time_stage",
-    "llmoe_layer_load", "llmoe_model_signs", "llmoe_last_error",
+    "llmoe_layer_load", "llmoe_model_signs", "llmoe_dense_create", "llmoe_dense_destroy", "llmoe_dense_forward",
+    "llmoe_last_error",
 ]
 
 STAGES = ["quant", "router", "route", "dispatch", "gate_up", "fwht", "down", "combine"]
@@ -84,6 +85,9 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.llmoe_last_error.restype = ctypes.c_char_p
     lib.llmoe_layer_load.argtypes = [ctypes.c_char_p, i, i, ctypes.POINTER(ctypes.c_void_p)]
     lib.llmoe_model_signs.argtypes = [ctypes.c_char_p, vp, i]
+    lib.llmoe_dense_create.argtypes = [i, i, i, vp, sz, i, ctypes.POINTER(ctypes.c_void_p)]
+    lib.llmoe_dense_destroy.argtypes = [vp]
+    lib.llmoe_dense_forward.argtypes = [vp, vp, vp, vp, i, vp, i, vp]
     lib.llmoe_layer_create.argtypes = [ctypes.POINTER(LayerDesc), vp, sz, vp, vp, vp, vp, vp,
                                        ctypes.POINTER(ctypes.c_void_p)]
     lib.llmoe_layer_destroy.argtypes = [vp]
@@ -271,6 +275,39 @@ def quantize_a8(x, stream=None):
     sm = torch.empty((rows, cols // 128), dtype=torch.int32, device=x.device)
     _check(load_library().llmoe_quantize_a8(_ptr(x), rows, cols, _ptr(q), _ptr(s), _ptr(sm), _stream(stream)))
     return q, s, sm
+
+
+class Dense:
+    """A dense W.A8 projection [rows, 2048] resident in HBM (llmoe_dense_*), packlib "i8" blob."""
+
+    def __init__(self, blob: np.ndarray, rows: int, bits: int, k: int = 2048, max_tokens: int = 4096):
+        self.lib = load_library()
+        self.rows, self.k = rows, k
+        blob = np.ascontiguousarray(blob, dtype=np.uint8)
+        h = ctypes.c_void_p()
+        _check(self.lib.llmoe_dense_create(rows, k, bits, _ptr(blob), blob.nbytes, max_tokens, ctypes.byref(h)))
+        self.handle = h
+
+    def forward(self, xq, xs, xsum, out=None, accumulate: bool = False, stream=None):
+        """y = W A8(x) (or out += that with accumulate): xq int8 [T, 2048], xs fp32 / xsum int32 [T, 16]."""
+        import torch
+        T = xq.shape[0]
+        if out is None:
+            out = torch.empty((T, self.rows), dtype=torch.float32, device=xq.device)
+        _check(self.lib.llmoe_dense_forward(self.handle, _ptr(xq), _ptr(xs), _ptr(xsum), T, _ptr(out),
+                                            int(accumulate), _stream(stream)))
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.llmoe_dense_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def time_stage_layers(layers, stage: str, reps: int = 20, stream=None) -> float:

@@ -12,7 +12,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent.parent
 CSRC = PKG.parent / "csrc"
-SOURCES = ["api.hip", "expert_gemm.hip", "tiled_gemm.hip", "act.hip", "route.hip", "relayout.hip", "loader.cpp"]
+SOURCES = ["api.hip", "expert_gemm.hip", "tiled_gemm.hip", "act.hip", "route.hip", "relayout.hip", "dense.hip", "loader.cpp"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",

@@ -602,6 +602,43 @@ int orc_reference_f64(const orc_layer* L, const float* x, int T, const int32_t* 
 /* ---- combine + un-rotation + residual + next-layer norm / rotation / A8 (engine/ops.cu:507-549) ---------------
  * Unnormalised Sylvester FWHT of n values, stages h = 1, 2, ..., n/2 ascending (engine/ops.cu:458-474 and the
  * bits 8-10 stages of :477-505 run in the same ascending order). */
+/* Dense W.A8 projection (engine/engine.cu:380-383, :425, :434): one matrix, every token, the same integer core
+ * and fp32 epilogue as the experts (orc_group_products, row_epilogue); accumulate adds to y (fp32 add). */
+int orc_dense(const uint8_t* blob, int R, int K, int bits, const int8_t* xq, const float* xs, const int32_t* xsum,
+              int T, float* y, int accumulate, int nthreads) {
+    if (orc_tile_wbytes(bits) < 0 || R % 16 || K % GROUP) return -1;
+    const int G = K / GROUP;
+    uint8_t* c = (uint8_t*)malloc((size_t)R * K);
+    uint8_t* z = (uint8_t*)malloc((size_t)R * G);
+    uint16_t* s = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)R * G);
+    if (!c || !z || !s) { free(c); free(z); free(s); return -2; }
+    orc_unpack_i8(blob, R, K, bits, c, s, z);
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#else
+    (void)nthreads;
+#endif
+    int err = 0;
+#pragma omp parallel num_threads(nthreads) reduction(| : err)
+    {
+        int32_t* P = (int32_t*)malloc(sizeof(int32_t) * (size_t)R * G);
+        if (!P) err |= 1;
+#pragma omp for schedule(static)
+        for (int t = 0; t < T; ++t) {
+            if (!P) continue;
+            orc_group_products(c, z, R, K, xq + (size_t)t * K, xsum + (size_t)t * G, P);
+            for (int r = 0; r < R; ++r) {
+                const float v = row_epilogue(P + (size_t)r * G, s + (size_t)r * G, xs + (size_t)t * G, G);
+                float* yo = y + (size_t)t * R + r;
+                *yo = accumulate ? *yo + v : v;
+            }
+        }
+        free(P);
+    }
+    free(c); free(z); free(s);
+    return err ? -2 : 0;
+}
+
 static void fwht_n(float* v, int n) {
     for (int h = 1; h < n; h <<= 1)
         for (int j = 0; j < n; ++j)

@@ -81,6 +81,11 @@ int orc_reference_f64(const orc_layer* L, const float* x, int T, const int32_t* 
 
 /* Combine + un-rotation + residual add + the next layer's RMSNorm, rotation and A8 (engine/ops.cu:507-549), H = 2048:
  * h [T, 2048] is updated in place; q/s/sum receive the next layer's A8 input. */
+/* Dense W.A8 projection (engine/engine.cu:380-383, :425, :434; the expert GEMM's integer core and fp32 epilogue
+ * with one matrix): y[t, r] = row_epilogue(P[r, :, t]) for the [R, K] packlib-i8 matrix, or y += that. */
+int orc_dense(const uint8_t* blob, int R, int K, int bits, const int8_t* xq, const float* xs, const int32_t* xsum,
+              int T, float* y, int accumulate, int nthreads);
+
 void orc_combine_norm(const float* Y, const int32_t* tok_slots, int T, int nk, int K1, const float* signs, float eps,
                       float* h, int8_t* q, float* s, int32_t* sum);
 

@@ -52,6 +52,8 @@ def lib() -> ctypes.CDLL:
         L.orc_reference_f64.argtypes = [ctypes.POINTER(OrcLayer), vp, i, vp, vp, vp, i]
         L.orc_reference_f64.restype = i
         L.orc_combine_norm.argtypes = [vp, vp, i, i, i, vp, f, vp, vp, vp, vp]
+        L.orc_dense.argtypes = [vp, i, i, i, vp, vp, vp, i, vp, i, i]
+        L.orc_dense.restype = i
         _lib = L
     return _lib
 
@@ -180,6 +182,20 @@ def combine_norm(Y, tok_slots, nk, signs, eps, h):
     lib().orc_combine_norm(_p(Y), _p(tok_slots), T, nk, K1, _p(np.ascontiguousarray(signs, np.float32)), eps, _p(hn),
                            _p(q), _p(s), _p(sm))
     return hn, q, s, sm
+
+
+def dense(blob, R, K, bits, xq, xs, xsum, y=None, nthreads=0):
+    """Dense W.A8 projection of the A8 rows (xq, xs, xsum) by the [R, K] packlib-i8 matrix: y = epilogue(P), or,
+    with y given, y + epilogue(P) (a new array)."""
+    blob = np.ascontiguousarray(blob, np.uint8)
+    xq = np.ascontiguousarray(xq, np.int8)
+    T = xq.shape[0]
+    out = np.zeros((T, R), np.float32) if y is None else np.array(y, np.float32, copy=True)
+    rc = lib().orc_dense(_p(blob), R, K, bits, _p(xq), _p(np.ascontiguousarray(xs, np.float32)),
+                         _p(np.ascontiguousarray(xsum, np.int32)), T, _p(out), 0 if y is None else 1, nthreads)
+    if rc:
+        raise RuntimeError(f"orc_dense: {rc}")
+    return out
 
 
 class Layer:

@@ -98,6 +98,20 @@ def route_case():
     return logits, bias
 
 
+DENSE = dict(R=512, K=2048, T=8)
+
+
+def dense_case(bits: int):
+    """A dense [R, K] matrix in the distribution of engine/tests/gen_dense_case.py (fp16 scales
+    U(0.5, 1.5) * 2 / 2^b * 0.05, zeros within 2 of 2^b / 2) and T fp16-valued token rows."""
+    R, K, T = DENSE["R"], DENSE["K"], DENSE["T"]
+    c = codes(3000 + bits, (R, K), bits)
+    s = (uniform(3001 + bits, (R, K // 128), 0.5, 1.5) * 2.0 / 2 ** bits * 0.05).astype(np.float16)
+    z = (codes(3002 + bits, (R, K // 128), 2).astype(np.int32) + 2 ** bits // 2 - 2).astype(np.uint8)
+    x = normal(3003 + bits, (T, K)).astype(np.float16).astype(np.float32)
+    return c, s, z, x
+
+
 def moe_case():
     """Tiny routed-expert layer in the format gen_moe_case.py builds: logical matrices per expert, tokens,
     routing, weights."""

@@ -6,7 +6,9 @@ never the reference. Functions used:
   quant/packlib.py:167-197 pack_matrix_i8, :98-102 gu_row_perm
   engine/tests/gen_moe_case.py:20-36 dequant / a8 / hadamard, :77-93 the per-slot reference loop (restated
       here around those helpers, since main() needs model files)
-  quant/s03_teacher_pass.py:132-146 route (with a duck-typed gate)"""
+  quant/s03_teacher_pass.py:132-146 route (with a duck-typed gate)
+  engine/tests/gen_dense_case.py:20-25 the dense reference Y = A8(x) @ dequant(W)^T (restated around the helpers,
+      since the script parses arguments and writes files)"""
 from __future__ import annotations
 
 import os
@@ -85,7 +87,19 @@ def moe_fixture():
                         blob_digest=np.array(gen.digest(*[blobs[k] for k in sorted(blobs)])))
 
 
+def dense_fixture():
+    out = {}
+    for b in (4, 8):
+        c, s, z, x = gen.dense_case(b)
+        Wd = (c.astype(np.float32) - np.repeat(z, 128, -1)) * np.repeat(s.astype(np.float32), 128, -1)
+        out[f"ref{b}"] = (GM.a8(x) @ Wd.T).astype(np.float32)
+        out[f"blob_digest{b}"] = np.array(gen.digest(PL.pack_matrix_i8(c, s, z, b)))
+        out[f"in_digest{b}"] = np.array(gen.digest(c, s, z, x))
+    np.savez_compressed(HERE / "dense_case.npz", **out)
+
+
 if __name__ == "__main__":
+    dense_fixture()
     packlib_fixture()
     a8_fwht_fixture()
     route_fixture()

@@ -110,3 +110,14 @@ def test_model_signs(lib, tmp_path):
     out = np.zeros(2048, np.float32)
     assert llmoe.load_library().llmoe_model_signs(str(tmp_path).encode(), out.ctypes.data, 2048) == 0
     np.testing.assert_array_equal(out, ref["signs"])
+
+
+def test_dense_create_rejects(lib):
+    """llmoe_dense_create validates its shape and blob before any GPU work."""
+    h = ctypes.c_void_p()
+    blob = np.zeros(16, np.uint8)
+    for rows, k, bits in ((512, 1024, 8), (100, 2048, 8), (512, 2048, 5)):
+        rc = lib.llmoe_dense_create(rows, k, bits, blob.ctypes.data, blob.nbytes, 32, ctypes.byref(h))
+        assert rc == llmoe.LLMOE_EINVAL, (rows, k, bits)
+    rc = lib.llmoe_dense_create(512, 2048, 8, blob.ctypes.data, blob.nbytes, 32, ctypes.byref(h))
+    assert rc == llmoe.LLMOE_EINVAL and "blob" in lib.llmoe_last_error().decode()

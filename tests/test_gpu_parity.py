@@ -6,12 +6,16 @@ as well, since both sides run the same fp32 operation sequence -- and, as the co
 1e-3 relative (FP_TOL) of the oracle.
 """
 import sys
+from pathlib import Path
 
 import numpy as np
 import pytest
 
 import oracle
 from llmoe import Layer, synth
+
+sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+import gen  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -240,6 +244,32 @@ def test_layer_load_matches_create(gpu, tmp_path):
     assert np.array_equal(a.view(np.uint32), r["out"].view(np.uint32))
     Gl.close()
     Gc.close()
+
+
+@pytest.mark.parametrize("T,bits,R", [(1, 8, 3072), (16, 4, 512), (32, 2, 1024), (32, 3, 512), (100, 8, 512),
+                                      (300, 4, 768), (77, 2, 256)])
+def test_dense_bit_exact(gpu, T, bits, R):
+    """llmoe_dense_forward (streamed for T <= 32, tiled above) == orc_dense, store and accumulate."""
+    import torch
+    from llmoe import Dense
+    say(f"[dense] T={T} bits={bits} R={R}")
+    c, s_, z = gen.matrix(4000 + bits + R, R, 2048, bits)
+    blob = oracle.pack_i8(c, s_, z, bits)
+    x = synth.make_x(4100 + T, T)
+    xq, xs, xsum = oracle.quant_a8(x)
+    D = Dense(blob, R, bits, max_tokens=512)
+    dx = [to_dev(a, gpu) for a in (xq, xs, xsum)]
+    y = D.forward(*dx)
+    torch.cuda.synchronize()
+    ref = oracle.dense(blob, R, 2048, bits, xq, xs, xsum)
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), ref.view(np.uint32)), "dense not bit-exact"
+    y0 = np.random.default_rng(T).standard_normal((T, R)).astype(np.float32)
+    yd = to_dev(y0, gpu)
+    D.forward(*dx, out=yd, accumulate=True)
+    torch.cuda.synchronize()
+    ref2 = oracle.dense(blob, R, 2048, bits, xq, xs, xsum, y=y0)
+    assert np.array_equal(yd.cpu().numpy().view(np.uint32), ref2.view(np.uint32)), "dense accumulate not bit-exact"
+    D.close()
 
 
 def test_router_logits_bit_exact(gpu):

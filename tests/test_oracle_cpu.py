@@ -325,3 +325,28 @@ def test_combine_norm_closed_form():
     # the rotation is orthogonal: ||Q^T v|| = ||v|| (checked on the un-rotation increment)
     inc = (hn - h).astype(np.float64)
     np.testing.assert_allclose(np.linalg.norm(inc, axis=1), np.linalg.norm(x, axis=1), rtol=1e-5)
+
+
+# ---- dense W.A8 projection (engine/engine.cu:380-383, :425, :434; KAT engine/tests/gen_dense_case.py) -------
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dense_against_reference(bits):
+    f = fixture("dense_case.npz")
+    c, s, z, x = gen.dense_case(bits)
+    assert gen.digest(c, s, z, x) == str(f[f"in_digest{bits}"])
+    R, K = c.shape
+    blob = O.pack_i8(c, s, z, bits)
+    assert gen.digest(blob) == str(f[f"blob_digest{bits}"])        # same bytes as the reference's packlib
+    xq, xs, xsum = O.quant_a8(x)
+    y = O.dense(blob, R, K, bits, xq, xs, xsum)
+    ref = f[f"ref{bits}"]                                            # A8(x) @ dequant(W)^T in fp32 (numpy)
+    # the exact value of the same sum, in fp64
+    xd = (xq.astype(np.float64).reshape(-1, K // 128, 128) * xs.astype(np.float64)[:, :, None]).reshape(-1, K)
+    wd = (c.astype(np.float64) - np.repeat(z, 128, -1)) * np.repeat(s.astype(np.float64), 128, -1)
+    exact = xd @ wd.T
+    scale = np.abs(exact).max()
+    assert np.abs(y - exact).max() <= 2e-6 * scale                  # one fp32 rounding per group
+    assert np.abs(ref - exact).max() <= 2e-6 * scale
+    assert np.abs(y - ref).max() <= 1e-3 * scale                     # the parity bar
+    # accumulate: y0 + epilogue, one fp32 add per element
+    y0 = gen.normal(3100, y.shape).astype(np.float32)
+    np.testing.assert_array_equal(O.dense(blob, R, K, bits, xq, xs, xsum, y=y0), y0 + y)
