@@ -87,11 +87,13 @@ def stage_profile(G, fn, reps=20):
     return {k: float(np.median(v)) for k, v in acc.items()}
 
 
-def one_layer_config(llmoe, synth, torch, name, seed, T, mix, shared, pool, steps, warmup, nlayers=4):
+def one_layer_config(llmoe, synth, torch, name, seed, T, mix, shared, pool, steps, warmup, nlayers=4,
+                     zero_bias=False):
     """A step is one layer pass; consecutive steps cycle through `nlayers` independently seeded layers so the
-    weights (> 256 MB in total) stream from HBM, not from the last-level cache."""
+    weights (> 256 MB in total) stream from HBM, not from the last-level cache. zero_bias: the router runs with a
+    zero expert bias, so the experts are exchangeable and each token's top-8 is a uniformly random 8-subset."""
     dev = torch.device("cuda:0")
-    Ls = [synth.make_layer(seed + 1000 * i, mix=mix, shared=shared) for i in range(nlayers)]
+    Ls = [synth.make_layer(seed + 1000 * i, mix=mix, shared=shared, zero_bias=zero_bias) for i in range(nlayers)]
     Gs = [make_gpu_layer(llmoe, L, pool, T) for L in Ls]
     x = torch.from_numpy(synth.make_x(seed + 1, T)).to(dev)
     out = torch.empty((T, H), dtype=torch.float32, device=dev)
@@ -318,8 +320,8 @@ def main():
         return
     log("[bench] config 1 (headline)")
     c1, (L1, G1s, x1, _, _) = one_layer_config(llmoe, synth, torch, "config 1: 32 tokens, mixed 2/3/4-bit + W8A8 "
-                                              "shared, uniform-random routing (no pool)", 1, 32, "mixed", True, 256,
-                                              args.steps, args.warmup)
+                                              "shared, uniform-random routing (router x Wr with zero bias, no pool)",
+                                              1, 32, "mixed", True, 256, args.steps, args.warmup, zero_bias=True)
     c1["with_combine_norm"] = norm_step(llmoe, torch, G1s, x1, args.steps, args.warmup)
     configs = [c1]
     if not args.only_headline:

@@ -203,6 +203,45 @@ def test_tiled_units_bit_exact(gpu, T, mix, kind):
     G.close()
 
 
+@pytest.mark.parametrize("T,mix,shared,pool,kind", [
+    (512, "mixed", True, 48, None),       # config 2: router x Wr with outlier channels, block pool 48
+    (2048, "mixed", True, 256, "zipf"),   # one layer of config 3
+    (4096, 2, False, 256, "uniform"),     # config 4, 2-bit
+    (4096, 8, False, 256, "skewed"),      # config 4, 8-bit, 16 experts take half the slots
+])
+def test_full_size_batch_invariance(gpu, T, mix, shared, pool, kind):
+    """At the configs' full token counts the GPU layer runs every expert through the work lists and chunking of
+    that size; a token's output depends only on its own routing block, so the rows of a few whole 32-token
+    blocks must equal, bit for bit, the oracle run on those blocks alone (indices, weights and outputs)."""
+    say(f"[full size] T={T} mix={mix} shared={shared} pool={pool} {kind}")
+    L = synth.make_layer(7 + T, mix=mix, shared=shared, zero_bias=kind is not None)
+    x = synth.make_x(900 + T, T, outlier_frac=0.01 if mix == "mixed" else 0.0)
+    lg = None
+    if kind == "zipf":
+        lg = synth.logits_zipf(T + 3, T)
+    elif kind == "skewed":
+        lg = synth.logits_skewed(T + 3, T)
+    elif kind == "uniform":
+        lg = np.random.default_rng(T + 3).standard_normal((T, 256)).astype(np.float32)
+    G = make_gpu_layer(L, pool, max_tokens=T)
+    out = run_layer(G, x, gpu, logits=lg)
+    topk = G.read("topk", (T, 8), np.int32)
+    topw = G.read("topw", (T, 8), np.float32)
+    count = G.read("count", (256,), np.int32)   # routed slots per expert
+    G.close()
+    assert count.sum() == 8 * T
+    if T >= 2048:
+        assert (count > 64).sum() >= 8, "the case must run multi-chunk tiled experts"
+    nb = T // 32
+    blocks = [0, nb // 3, nb - 1]
+    rows = np.concatenate([np.arange(32 * b, 32 * b + 32) for b in blocks])
+    r = oracle.Layer(L).forward(x[rows], logits=None if lg is None else lg[rows], C=pool)
+    assert np.array_equal(topk[rows], r["topk"]), "expert indices differ"
+    assert np.array_equal(topw[rows].view(np.uint32), r["topw"].view(np.uint32)), "routing weights differ"
+    close(out[rows], r["out"], "out")
+    assert np.array_equal(out[rows].view(np.uint32), r["out"].view(np.uint32)), "output rows not bit-exact"
+
+
 @pytest.mark.parametrize("T,pool", [(32, 256), (200, 48)])
 def test_experts_norm_bit_exact(gpu, T, pool):
     """llmoe_experts_norm: combine + FWHT-2048 un-rotation + residual + next-layer RMSNorm / rotation / A8."""
