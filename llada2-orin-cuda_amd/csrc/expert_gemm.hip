@@ -268,14 +268,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
                     const v4i B1 = *reinterpret_cast<const v4i*>(br + 64);
                     xsc = bs[g * NTOK + col];
                     const int nxsum = bsum[g * NTOK + col];
-                    Cc = v4i{__mul24(zz[0], nxsum), __mul24(zz[1], nxsum), __mul24(zz[2], nxsum), __mul24(zz[3], nxsum)};
+                    Cc = v4i{__mul24(zz[0], nxsum) + I2F_BIAS, __mul24(zz[1], nxsum) + I2F_BIAS,
+                             __mul24(zz[2], nxsum) + I2F_BIAS, __mul24(zz[3], nxsum) + I2F_BIAS};
                     Cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, Cc, 0, 0, 0);
                     Cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, Cc, 0, 0, 0);
                 }
                 if constexpr (tau > 0) {
 #pragma unroll
                     for (int v = 0; v < 4; ++v)
-                        acc[0][v] = __builtin_fmaf(mul_f16_f32(swpp[v >> 1], v & 1, xsp), float(Cp[v]), acc[0][v]);
+                        acc[0][v] = __builtin_fmaf(mul_f16_f32(swpp[v >> 1], v & 1, xsp), biased_to_f32(Cp[v]), acc[0][v]);
                     asm volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[0][2]), "+v"(acc[0][3]));
                 }
                 if constexpr (tau < 4) {

@@ -120,6 +120,12 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     }
     return uint16_t(sign | h);
 }
+// int32 -> fp32 through the MFMA accumulator: a product that starts from I2F_BIAS (the bits of 1.5 * 2^23) ends as
+// the bits of the float 1.5 * 2^23 + P exactly when |P| < 2^22 (every group product: |c - z| <= 255, |xq| <= 127,
+// 128 terms), so one subtraction -- cheaper than v_cvt_f32_i32 on gfx950 -- returns float(P) exactly.
+constexpr int I2F_BIAS = 0x4B400000;
+__device__ __forceinline__ float biased_to_f32(int c) { return __int_as_float(c) - 12582912.0f; }
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
 }

@@ -275,6 +275,14 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
             const int n = nt * 16 + col;
             return reinterpret_cast<const v4i*>(bg + n * GROUP + (((q + 4 * half) ^ (n & 7)) << 4));
         };
+        // with several token tiles the group's fp16 weight scales are converted once and multiplied per tile
+        float swf[S][4];
+        if constexpr (NTILE > 1) {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) swf[s][v] = f16_bits_to_f32(swp[s][v >> 1] >> (16 * (v & 1)));
+        }
         v4i Cp[S];
         float xsp = 0.0f;
         v4i Bn0 = *bptr(0, 0), Bn1 = *bptr(0, 1);
@@ -298,10 +306,10 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
                     if constexpr (BITS >= 4)
-                        Cc[s] = v4i{__mul24(zz[s][0], nsum), __mul24(zz[s][1], nsum), __mul24(zz[s][2], nsum),
-                                    __mul24(zz[s][3], nsum)};
+                        Cc[s] = v4i{__mul24(zz[s][0], nsum) + I2F_BIAS, __mul24(zz[s][1], nsum) + I2F_BIAS,
+                                    __mul24(zz[s][2], nsum) + I2F_BIAS, __mul24(zz[s][3], nsum) + I2F_BIAS};
                     else
-                        Cc[s] = v4i{0, 0, 0, 0};
+                        Cc[s] = v4i{I2F_BIAS, I2F_BIAS, I2F_BIAS, I2F_BIAS};
                     Cc[s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0[s], B0, Cc[s], 0, 0, 0);
                 }
 #pragma unroll
@@ -311,9 +319,11 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
 #pragma unroll
-                    for (int v = 0; v < 4; ++v)
-                        acc[s][nt - 1][v] = __builtin_fmaf(mul_f16_f32(swp[s][v >> 1], v & 1, xsp), float(Cp[s][v]),
-                                                           acc[s][nt - 1][v]);
+                    for (int v = 0; v < 4; ++v) {
+                        // scale_w * scale_x: one fp32 product either way (the fp16 scale converts exactly)
+                        const float sc = NTILE > 1 ? swf[s][v] * xsp : mul_f16_f32(swp[s][v >> 1], v & 1, xsp);
+                        acc[s][nt - 1][v] = __builtin_fmaf(sc, biased_to_f32(Cp[s][v]), acc[s][nt - 1][v]);
+                    }
                     // materialise the tile's accumulators here: otherwise the compiler defers the fp32 chains
                     // and keeps every tile's MFMA results live
                     asm volatile("" : "+v"(acc[s][nt - 1][0]), "+v"(acc[s][nt - 1][1]), "+v"(acc[s][nt - 1][2]),
