@@ -60,7 +60,7 @@ __global__ void __launch_bounds__(256) dense_plan_kernel(int T, int R, int bits,
         if (threadIdx.x == 0) n_units[0] = nit * nrb;
         return;
     }
-    const int nch = tiled_chunks(T), per = tiled_per(T), nrb = R / (16 * TILED_WAVES * tiled_spw(bits));
+    const int nch = tiled_chunks(T), per = tiled_per(T), nrb = R / (16 * tiled_waves(false) * tiled_spw(false, bits));
     for (int j = threadIdx.x; j < nch; j += blockDim.x) units[j] = Item{0, j * per, min(per, T - j * per), 0};
     const long long N = (long long)nch * nrb;
     for (int w = threadIdx.x; w <= G; w += blockDim.x) {

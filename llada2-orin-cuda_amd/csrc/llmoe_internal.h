@@ -36,14 +36,16 @@ constexpr int MAX_UNITS_PER_ITEM = 16;   // gemm_row_blocks(false, 8)
 
 // Tiled GEMM (experts with many tokens): a work unit is a chunk of <= TILED_NTOK slots of one expert and a
 // range of row blocks (Item.rb = first | count << 16); the workgroup stages the chunk's activations in LDS once
-// and its TILED_WAVES waves stream tiled_spw strips each per row block. An expert takes tiled units when it has
+// and its tiled_waves waves stream tiled_spw strips each per row block. An expert takes tiled units when it has
 // more than TILED_MIN slots, otherwise streamed units of 16 slots.
+// K = 2048 (gate_up, dense): 8 waves of 2 strips (1 for 8-bit codes). K = 512 (down): 16 waves of 1 strip, whose
+// registers fit 4 waves per SIMD (the vector issue rate per SIMD grows with the waves it can pick from).
 constexpr int TILED_NTOK = 64;
 constexpr int TILED_MIN = 16;
-constexpr int TILED_WAVES = 8;
-__host__ __device__ constexpr int tiled_spw(int bits) { return bits == 8 ? 1 : 2; }
+__host__ __device__ constexpr int tiled_waves(bool down) { return down ? 16 : 8; }
+__host__ __device__ constexpr int tiled_spw(bool down, int bits) { return down ? 1 : bits == 8 ? 1 : 2; }
 __host__ __device__ constexpr int tiled_row_blocks(bool down, int bits) {
-    return (down ? 2048 : 1024) / (16 * TILED_WAVES * tiled_spw(bits));
+    return (down ? 2048 : 1024) / (16 * tiled_waves(down) * tiled_spw(down, bits));
 }
 // chunks of an expert with c slots: n = ceil(c / TILED_NTOK) chunks of `per` slots (a multiple of 16), the last
 // one shorter

@@ -191,7 +191,7 @@ __device__ void emit_shared_units(int E, int T, int K, int ntok, int bits, Item*
 // unpacking, the weight stream) plus a per-tile part (MFMAs and the fp32 epilogue), as measured on MI355X for
 // each code width (8-bit row blocks have half the rows)
 __device__ __forceinline__ int rb_cost(int bits, int nt, bool down) {
-    if (down) return bits == 8 ? 42 + 10 * nt : bits == 3 ? 42 + 21 * nt : bits == 4 ? 48 + 20 * nt : 36 + 20 * nt;
+    if (down) return bits == 8 ? 73 + 17 * nt : bits == 3 ? 37 + 18 * nt : bits == 4 ? 34 + 19 * nt : 30 + 18 * nt;
     return bits == 8 ? 64 + 35 * nt : bits == 3 ? 134 + 66 * nt : bits == 4 ? 78 + 72 * nt : 70 + 70 * nt;
 }
 // the chunk's row-block task cost and row-block count of both GEMMs, packed (cost << 8 | count) for the planner

@@ -3,12 +3,12 @@
 // :364-383): per 128-group g, P_g = sum code xq - zero Sxq exact in int32, then
 // acc = fma(scale_w scale_x, float(P_g), acc) for g ascending from 0.
 //
-// Work unit: <= TILED_NTOK (64) slots of one expert and a range of row blocks. The workgroup (8 waves) first
+// Work unit: <= TILED_NTOK (64) slots of one expert and a range of row blocks. The workgroup (8 waves; 16 for down) first
 // copies the chunk's int8 activation rows for the WHOLE reduction (64 x K bytes, XOR-swizzled 16-byte chunks so
 // the MFMA operand reads are conflict-free), their scales and sums into LDS, then every wave streams its own
 // tiled_spw(bits) 16-row strips of each row block through registers: each 16x128 weight tile is unpacked once
 // into MFMA A operands and used for all 4 token tiles, and the fp32 accumulators of the (strip, token tile)
-// pairs stay in registers until the fused epilogue. No barrier inside a row block, so the 8 waves (2 per SIMD)
+// pairs stay in registers until the fused epilogue. No barrier inside a row block, so the waves (2 per SIMD; 4 for down)
 // drift freely and one wave's MFMAs overlap the other's vector epilogue.
 // Zero points: for 2/3-bit codes the zero is subtracted while unpacking (a v_perm_b32 lookup of c - z), so the
 // MFMA accumulates from 0; 4-bit codes and 8-bit codes (stored c - 128) start the MFMA from the zero term
@@ -24,8 +24,9 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 
-constexpr int NW = TILED_WAVES;                 // waves per workgroup
-constexpr int NTHREADS = NW * 64;
+// waves and threads per workgroup of the GEMM with reduction K
+__host__ __device__ constexpr int nw_for(int K) { return tiled_waves(K == 512); }
+__host__ __device__ constexpr int nthreads_for(int K) { return 64 * nw_for(K); }
 constexpr int MAX_TILE = TILED_NTOK / 16;       // 16-token tiles per chunk
 // LDS: activations [group][token][128 B] (16-byte chunk c of token n at ((c ^ (n & 7)) * 16)), then fp32 scales
 // and negated int32 sums [group][token], then the chunk's row table [token]
@@ -158,6 +159,7 @@ __device__ __forceinline__ float mul_f16_f32(uint32_t packed, int hi, float x) {
 // issues all of its activation loads back to back. Returns after the workgroup barrier.
 template <int K>
 __device__ __forceinline__ void stage_chunk(const GemmArgs& a, const Item& it, uint8_t* lds) {
+    constexpr int NTHREADS = nthreads_for(K);
     constexpr int G = K / GROUP, PER = TILED_NTOK * (K / 16) / NTHREADS;
     constexpr int PS = (G * TILED_NTOK + NTHREADS - 1) / NTHREADS;
     static_assert(PER * NTHREADS == TILED_NTOK * (K / 16) && TILED_NTOK == 64, "staging split");
@@ -217,7 +219,7 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
                                                const uint8_t* lds, int rb) {
     constexpr bool DOWN = MODE == GEMM_DOWN;
     constexpr int NSB = DOWN ? 1 : 4, K = NSB * SB_K, G = K / GROUP;
-    constexpr int S = tiled_spw(BITS);
+    constexpr int S = tiled_spw(DOWN, BITS), NW = nw_for(K);
     constexpr size_t SBB = sb_bytes(BITS);
     const int lane = threadIdx.x & 63, q = lane >> 4, col = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -398,7 +400,7 @@ __device__ __forceinline__ void tiled_body(const GemmArgs& a, const Item& it, ui
 // Workgroup w runs the row-block tasks tstart[w] .. tstart[w + 1] (chunk-major, so the chunk's activations are
 // staged once per run of its row blocks).
 template <int MODE>
-__global__ void __launch_bounds__(NTHREADS) tiled_gemm(GemmArgs a) {
+__global__ void __launch_bounds__(nthreads_for(MODE == GEMM_DOWN ? 512 : 2048)) tiled_gemm(GemmArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int CMASK = (1 << TASK_RB_SHIFT) - 1;
     const int s0 = a.tstart[blockIdx.x], s1 = a.tstart[blockIdx.x + 1];
@@ -407,7 +409,8 @@ __global__ void __launch_bounds__(NTHREADS) tiled_gemm(GemmArgs a) {
     for (int c = c0; c < c1 || (c == c1 && r1 > 0); ++c) {
         const Item it = a.items[c];
         const int bits = a.bits[it.expert];
-        const int nrb = MODE == GEMM_DENSE ? a.R / (16 * NW * tiled_spw(bits)) : tiled_row_blocks(MODE == GEMM_DOWN, bits);
+        const int nrb = MODE == GEMM_DENSE ? a.R / (16 * tiled_waves(false) * tiled_spw(false, bits))
+                                           : tiled_row_blocks(MODE == GEMM_DOWN, bits);
         const int rb0 = c == c0 ? r0 : 0, rb1 = c == c1 ? r1 : nrb;
         if (rb0 >= rb1) continue;
 #ifdef LLMOE_TILED_TRACE
@@ -459,7 +462,7 @@ int grid_t() {
         hipError_t e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (e == hipSuccess)
-            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kptr<MODE>(), NTHREADS,
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kptr<MODE>(), nthreads_for(MODE == GEMM_DOWN ? 512 : 2048),
                                                              lds_bytes_for(MODE == GEMM_DOWN ? 512 : 2048));
         if (e != hipSuccess) return 0;
         grid = cus * (per_cu > 0 ? per_cu : 1);
@@ -471,7 +474,8 @@ template <int MODE>
 hipError_t launch_t(const GemmArgs& a, hipStream_t st) {
     const int grid = grid_t<MODE>();
     if (!grid) return hipErrorInvalidDevice;
-    tiled_gemm<MODE><<<grid, NTHREADS, lds_bytes_for(MODE == GEMM_DOWN ? 512 : 2048), st>>>(a);
+    constexpr int K = MODE == GEMM_DOWN ? 512 : 2048;
+    tiled_gemm<MODE><<<grid, nthreads_for(K), lds_bytes_for(K), st>>>(a);
     return hipGetLastError();
 }
 
