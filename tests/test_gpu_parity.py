@@ -347,3 +347,51 @@ def test_external_dispatch(gpu):
     check_full(G, r, T, K, True)
     assert np.array_equal(out.cpu().numpy().view(np.uint32), r["out"].view(np.uint32))
     G.close()
+
+
+@pytest.mark.parametrize("T,pool", [(32, 256), (200, 48)])
+def test_hip_graph_replays(gpu, T, pool):
+    """The layer forward and a dense projection captured in one HIP graph: every replay, with eager calls on other
+    inputs and host synchronisations in between, reproduces the eager results bit for bit (the calls allocate,
+    clear and synchronise nothing, and keep no host state between launches)."""
+    import torch
+    from llmoe import Dense
+    say(f"[graph] T={T} pool={pool}")
+    L = layer_for("mixed", True)
+    G = make_gpu_layer(L, pool)
+    R = 1024
+    c, s_, z = gen.matrix(4500, R, 2048, 8)
+    D = Dense(oracle.pack_i8(c, s_, z, 8), R, 8, max_tokens=256)
+    x = to_dev(synth.make_x(60 + T, T), gpu)
+    x2 = to_dev(synth.make_x(61 + T, T), gpu)
+    xq, xs, xsum = (to_dev(a, gpu) for a in oracle.quant_a8(synth.make_x(62 + T, T)))
+    out = torch.empty((T, 2048), dtype=torch.float32, device=gpu)
+    y = torch.empty((T, R), dtype=torch.float32, device=gpu)
+    G.forward(x, out=out)
+    D.forward(xq, xs, xsum, out=y)
+    torch.cuda.synchronize()
+    ref_out, ref_y = out.clone(), y.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        G.forward(x, out=out)
+        D.forward(xq, xs, xsum, out=y)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        G.forward(x, out=out)
+        D.forward(xq, xs, xsum, out=y)
+    for i in range(4):
+        out.zero_()
+        y.zero_()
+        other = G.forward(x2)                  # eager work on the same layer object between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), ref_out.view(torch.int32)), f"replay {i}: layer output differs"
+        assert torch.equal(y.view(torch.int32), ref_y.view(torch.int32)), f"replay {i}: dense output differs"
+        assert not torch.equal(other, ref_out)
+    del g
+    D.close()
+    G.close()
