@@ -500,6 +500,66 @@ __global__ void __launch_bounds__(256) dispatch_kernel(int T, int E, int K, cons
     }
 }
 
+// Descending bitonic sort of one key per lane across the 64 lanes of a wave: lane i ends with the i-th largest.
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t k, int lane) {
+#pragma unroll
+    for (int s = 2; s <= 64; s <<= 1)
+#pragma unroll
+        for (int j = s >> 1; j > 0; j >>= 1) {
+            const uint64_t o = shfl_xor64(k, j);
+            // blocks of s lanes alternate direction (all descending at s = 64); the lower lane of a pair keeps
+            // the larger key in a descending block
+            const bool keep_max = ((lane & j) == 0) == ((lane & s) == 0);
+            k = keep_max ? (o > k ? o : k) : (o < k ? o : k);
+        }
+    return k;
+}
+
+// Decode selection without a pool (C = E): one token per workgroup, thread e scores expert e (router partials
+// summed in chunk order, sigmoid, + bias), each wave sorts its 64 keys, wave 0 sorts the four waves' leaders and
+// writes the top-K, the routing weights (engine/ops.cu:298-321) and the token masks. The same keys and the same
+// fp32 operation order as select_kernel, spread over T workgroups: the selection is latency-bound, and one token
+// per workgroup puts T times more waves on it.
+__global__ void __launch_bounds__(256) select_token_kernel(const float* __restrict__ part, int nchunks,
+                                                           const float* __restrict__ bias, int T, int E, int K,
+                                                           float rscale, int* __restrict__ topk,
+                                                           float* __restrict__ topw, DecodeState ds) {
+    __shared__ float sig_s[MAXE];
+    __shared__ uint64_t lead[4 * 8];
+    const int t = blockIdx.x, e = threadIdx.x, lane = e & 63, w = e >> 6;
+    uint64_t key = 0ull;
+    if (e < E) {
+        float p[ROUTER_KC];
+#pragma unroll
+        for (int c = 0; c < ROUTER_KC; ++c) p[c] = c < nchunks ? part[(size_t(c) * T + t) * E + e] : 0.0f;
+        float l = p[0];
+#pragma unroll
+        for (int c = 1; c < ROUTER_KC; ++c)
+            if (c < nchunks) l = l + p[c];
+        const float sv = sigmoid_f32(l);
+        sig_s[e] = sv;
+        key = sel_key(sv + bias[e], e);
+    }
+    key = wave_sort_desc(key, lane);
+    if (lane < 8) lead[w * 8 + lane] = key;
+    __syncthreads();
+    if (w == 0) {
+        uint64_t k2 = lane < 32 ? lead[lane] : 0ull;
+        k2 = wave_sort_desc(k2, lane);
+        const int ex = key_index(k2);
+        const float sk = lane < K ? sig_s[ex] : 0.0f;
+        float wsum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (k < K) wsum = wsum + __shfl(sk, k);
+        if (lane < K) {
+            topk[size_t(t) * K + lane] = ex;
+            topw[size_t(t) * K + lane] = sk / (wsum + 1e-20f) * rscale;
+            atomicOr(&ds.tmask[ex], 1u << t);
+        }
+    }
+}
+
 // grid ceil(T/8), 256 threads: pool membership (POOL: from blockmax of score_kernel), top-K of 8 tokens, routing
 // weights, token masks (engine/ops.cu:256-327, quant/s03_teacher_pass.py:132-146). Without the pool the scores
 // come straight from the router partials (summed in chunk order, as score_kernel does).
@@ -912,7 +972,7 @@ hipError_t launch_decode_route(const float* part, int nchunks, const float* bias
         score_kernel<<<T, 256, 0, st>>>(part, nchunks, bias, T, E, 1, sig, blockmax);
         select_kernel<true><<<(T + 7) / 8, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, rscale, topk, topw, ds);
     } else {
-        select_kernel<false><<<(T + 7) / 8, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, rscale, topk, topw, ds);
+        select_token_kernel<<<T, 256, 0, st>>>(part, nchunks, bias, T, E, K, rscale, topk, topw, ds);
     }
     const DispatchOut d{has_shared, 16, bits, count, start, units_gu, units_dn, n_units, slot_token, slot_weight,
                         tok_slots};
