@@ -1,12 +1,13 @@
 #!/usr/bin/env python3
 """Benchmark of the LLaDA2 routed-expert MoE layer on one MI355X through libllmoe.so.
 
-Headline workload (value): BASELINE config 1 -- one MoE layer, 32 tokens (one denoising block), hidden 2048,
-256 routed experts at the shipped 2/3/4-bit mix (61/34/6 %), top-8 of sigmoid(x Wr) + bias, plus the W8A8
+Headline workload (value): config 1 -- one MoE layer, 32 tokens (one denoising block), hidden 2048, 256
+routed experts at the shipped 2/3/4-bit mix (61/34/6 %), uniform-random top-8 of sigmoid(x Wr), plus the W8A8
 shared expert; a step is one full layer pass (A8 of x -> router -> routing + dispatch -> gate_up -> FWHT-512 + A8
 -> down -> combine) with x already resident in HBM. Also measured (fields "configs"): config 0 (32 tokens, all
-4-bit, block pool 48, no shared expert) and config 3 (2048 tokens through a stack of 20 independently seeded
-layers with Zipf(1.1) expert load).
+4-bit, block pool 48, no shared expert), config 2 (512 tokens), config 3 (2048 tokens through a stack of 20
+independently seeded layers with Zipf(1.1) expert load), config 4 (4096 tokens at 2/4/8 bits, uniform and skewed
+routing) and the dense projection at 32 and 2048 tokens.
 
 Roofline: the dominant kernel is the gate_up expert GEMM (two thirds of the weight bytes); its algorithmic bytes
 per launch are the packed gate_up bytes of every expert the step touches (each streamed exactly once) plus the
@@ -302,8 +303,8 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true", help="run 512 MiB device copies first (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (expert sharding is described in "
-              "DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (expert parallelism is a design note "
+              "only); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
