@@ -515,30 +515,58 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t k, int lane) {
     return k;
 }
 
-// Decode selection without a pool (C = E): one token per workgroup, thread e scores expert e (router partials
-// summed in chunk order, sigmoid, + bias), each wave sorts its 64 keys, wave 0 sorts the four waves' leaders and
-// writes the top-K, the routing weights (engine/ops.cu:298-321) and the token masks. The same keys and the same
-// fp32 operation order as select_kernel, spread over T workgroups: the selection is latency-bound, and one token
-// per workgroup puts T times more waves on it.
+// Decode selection, one token per workgroup (engine/ops.cu:256-327): thread e scores expert e, each wave sorts
+// its 64 keys, wave 0 sorts the four waves' leaders and writes the top-K, the routing weights
+// (engine/ops.cu:298-321) and the token masks. Without the pool the scores come from the router partials (summed
+// in chunk order, then the sigmoid); with it from score_kernel's sigmoids, and expert e is in the block's pool
+// when fewer than C experts have a larger blockmax key (ties to the lower index): the four waves sort the
+// blockmax keys and each thread counts the larger ones by binary search. One token per workgroup puts T times
+// more waves on this latency-bound step than 8 tokens per workgroup.
+template <bool POOL>
 __global__ void __launch_bounds__(256) select_token_kernel(const float* __restrict__ part, int nchunks,
+                                                           const float* __restrict__ sig,
                                                            const float* __restrict__ bias, int T, int E, int K,
-                                                           float rscale, int* __restrict__ topk,
+                                                           int C, float rscale, int* __restrict__ topk,
                                                            float* __restrict__ topw, DecodeState ds) {
     __shared__ float sig_s[MAXE];
     __shared__ uint64_t lead[4 * 8];
+    __shared__ uint64_t pool_s[POOL ? MAXE : 1];
     const int t = blockIdx.x, e = threadIdx.x, lane = e & 63, w = e >> 6;
+    bool inpool = true;
+    if constexpr (POOL) {
+        const uint64_t pk = e < E ? (uint64_t(ds.blockmax[e]) << 32) | uint32_t(0xFFFF - e) : 0ull;
+        pool_s[w * 64 + lane] = wave_sort_desc(pk, lane);
+        __syncthreads();
+        int rank = 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {   // keys of the descending list v larger than pk
+            const uint64_t* a = pool_s + v * 64;
+            int lo = 0;
+#pragma unroll
+            for (int step = 32; step > 0; step >>= 1)
+                if (a[lo + step - 1] > pk) lo += step;
+            if (lo == 63 && a[63] > pk) lo = 64;
+            rank += lo;
+        }
+        inpool = rank < C;
+    }
     uint64_t key = 0ull;
     if (e < E) {
-        float p[ROUTER_KC];
+        float sv;
+        if constexpr (POOL) {
+            sv = sig[size_t(t) * E + e];
+        } else {
+            float p[ROUTER_KC];
 #pragma unroll
-        for (int c = 0; c < ROUTER_KC; ++c) p[c] = c < nchunks ? part[(size_t(c) * T + t) * E + e] : 0.0f;
-        float l = p[0];
+            for (int c = 0; c < ROUTER_KC; ++c) p[c] = c < nchunks ? part[(size_t(c) * T + t) * E + e] : 0.0f;
+            float l = p[0];
 #pragma unroll
-        for (int c = 1; c < ROUTER_KC; ++c)
-            if (c < nchunks) l = l + p[c];
-        const float sv = sigmoid_f32(l);
+            for (int c = 1; c < ROUTER_KC; ++c)
+                if (c < nchunks) l = l + p[c];
+            sv = sigmoid_f32(l);
+        }
         sig_s[e] = sv;
-        key = sel_key(sv + bias[e], e);
+        if (inpool) key = sel_key(sv + bias[e], e);
     }
     key = wave_sort_desc(key, lane);
     if (lane < 8) lead[w * 8 + lane] = key;
@@ -560,109 +588,6 @@ __global__ void __launch_bounds__(256) select_token_kernel(const float* __restri
     }
 }
 
-// grid ceil(T/8), 256 threads: pool membership (POOL: from blockmax of score_kernel), top-K of 8 tokens, routing
-// weights, token masks (engine/ops.cu:256-327, quant/s03_teacher_pass.py:132-146). Without the pool the scores
-// come straight from the router partials (summed in chunk order, as score_kernel does).
-template <bool POOL>
-__global__ void __launch_bounds__(256) select_kernel(const float* __restrict__ part, int nchunks,
-                                                     const float* __restrict__ sig, const float* __restrict__ bias,
-                                                     int T, int E, int K, int C, float rscale, int* __restrict__ topk,
-                                                     float* __restrict__ topw, DecodeState ds) {
-    __shared__ __align__(16) uint64_t key[MAXE];
-    __shared__ float sbias[MAXE];
-    __shared__ int inpool[MAXE];
-    __shared__ float sigl[8][MAXE];
-    const int tid = threadIdx.x;
-    if (tid < MAXE) {
-        sbias[tid] = tid < E ? bias[tid] : 0.0f;
-        if (POOL) key[tid] = tid < E ? (uint64_t(ds.blockmax[tid]) << 32) | uint32_t(0xFFFF - tid) : 0ull;
-    }
-    __syncthreads();
-    if (tid < E) {   // pool = the C largest keys: rank = number of larger keys
-        int rank = 0;
-        if (POOL) {
-            const uint64_t ke = key[tid];
-            const ulonglong2* k2 = reinterpret_cast<const ulonglong2*>(key);
-#pragma unroll 8
-            for (int j = 0; j < MAXE / 2; ++j) {
-                const ulonglong2 kk = k2[j];
-                rank += (kk.x > ke) + (kk.y > ke);
-            }
-        }
-        inpool[tid] = rank < C;
-    }
-    __syncthreads();
-    const int tl = tid >> 5, sub = tid & 31, t = blockIdx.x * 8 + tl;
-    const bool valid = t < T;
-    float sv[8];
-    if (valid && sub * 8 < E) {
-        if constexpr (POOL) {
-            const float4 a = *reinterpret_cast<const float4*>(sig + size_t(t) * E + sub * 8);
-            const float4 b = *reinterpret_cast<const float4*>(sig + size_t(t) * E + sub * 8 + 4);
-            sv[0] = a.x; sv[1] = a.y; sv[2] = a.z; sv[3] = a.w; sv[4] = b.x; sv[5] = b.y; sv[6] = b.z; sv[7] = b.w;
-        } else {
-            float4 p[ROUTER_KC][2];
-#pragma unroll
-            for (int c = 0; c < ROUTER_KC; ++c)
-                if (c < nchunks) {
-                    const float* pp = part + (size_t(c) * T + t) * E + sub * 8;
-                    p[c][0] = *reinterpret_cast<const float4*>(pp);
-                    p[c][1] = *reinterpret_cast<const float4*>(pp + 4);
-                }
-            float l[8] = {p[0][0].x, p[0][0].y, p[0][0].z, p[0][0].w, p[0][1].x, p[0][1].y, p[0][1].z, p[0][1].w};
-#pragma unroll
-            for (int c = 1; c < ROUTER_KC; ++c)
-                if (c < nchunks) {
-                    const float q8[8] = {p[c][0].x, p[c][0].y, p[c][0].z, p[c][0].w,
-                                         p[c][1].x, p[c][1].y, p[c][1].z, p[c][1].w};
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) l[j] = l[j] + q8[j];
-                }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) sv[j] = sigmoid_f32(l[j]);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sigl[tl][sub * 8 + j] = sv[j];
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sv[j] = 0.0f;
-    }
-    uint64_t best[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int ex = sub * 8 + j;
-        best[j] = valid && ex < E && inpool[ex] ? sel_key(sv[j] + sbias[ex], ex) : 0ull;
-    }
-    sort8(best);
-#pragma unroll 1
-    for (int o = 1; o < 32; o <<= 1) {
-        uint64_t other[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) other[k] = shfl_xor64(best[k], o);
-        merge8(best, other);
-    }
-    if (valid) {
-        float wsum = 0.0f, mine = 0.0f;
-        int mysel = 0;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if (k < K) {
-                const int ex = key_index(best[k]);
-                const float sk = sigl[tl][ex];
-                wsum = wsum + sk;
-                if (k == sub) {
-                    mine = sk;
-                    mysel = ex;
-                }
-            }
-        }
-        if (sub < K) {
-            topk[size_t(t) * K + sub] = mysel;
-            topw[size_t(t) * K + sub] = mine / (wsum + 1e-20f) * rscale;
-            atomicOr(&ds.tmask[mysel], 1u << t);
-        }
-    }
-}
 
 // Token masks of externally given routing. grid nb, 256 threads.
 __global__ void __launch_bounds__(256) masks_kernel(const int* __restrict__ topk, int T, int E, int K, int block,
@@ -970,9 +895,9 @@ hipError_t launch_decode_route(const float* part, int nchunks, const float* bias
     const DecodeState ds{blockmax, tmask};
     if (C < E) {
         score_kernel<<<T, 256, 0, st>>>(part, nchunks, bias, T, E, 1, sig, blockmax);
-        select_kernel<true><<<(T + 7) / 8, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, rscale, topk, topw, ds);
+        select_token_kernel<true><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, rscale, topk, topw, ds);
     } else {
-        select_token_kernel<<<T, 256, 0, st>>>(part, nchunks, bias, T, E, K, rscale, topk, topw, ds);
+        select_token_kernel<false><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, rscale, topk, topw, ds);
     }
     const DispatchOut d{has_shared, 16, bits, count, start, units_gu, units_dn, n_units, slot_token, slot_weight,
                         tok_slots};
