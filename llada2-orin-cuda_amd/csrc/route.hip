@@ -22,18 +22,19 @@ __device__ __forceinline__ uint32_t okey(float v) {        // order-preserving u
 }
 
 constexpr int RKW = 256;                                          // K per chunk (H = 2048)
-constexpr int RXS = RKW + 4;                                      // LDS row stride of the x slice
-constexpr int ROUTER_LDS = (32 * RXS + RKW * 16) * 4;
+constexpr int REW = 8;                                            // experts per workgroup
+constexpr int RXS = RKW + 4;                                      // LDS row stride of the x and Wr slices
+constexpr int ROUTER_LDS = (32 + REW) * RXS * 4;
 __global__ void __launch_bounds__(256) router_logits_kernel(const float* __restrict__ x, const float* __restrict__ Wr,
                                                             int T, int H, int E, float* __restrict__ part,
                                                             int8_t* __restrict__ q, float* __restrict__ qs,
                                                             int* __restrict__ qsum) {
     extern __shared__ __align__(16) float rl[];
     float* xs = rl;                       // [32][RXS]
-    float* ws = rl + 32 * RXS;            // [RKW][16]
-    const int e0 = blockIdx.x * 16, t0 = blockIdx.y * 32, c = blockIdx.z, kb = c * RKW;
+    float* ws = rl + 32 * RXS;            // [REW][RXS]: Wr slice transposed, k contiguous per expert
+    const int e0 = blockIdx.x * REW, t0 = blockIdx.y * 32, c = blockIdx.z, kb = c * RKW;
     const int tid = threadIdx.x;
-    float4 xv[8], wv[4];
+    float4 xv[8], wv[2];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {                                 // x: 32 x 256 floats as float4
         const int idx = tid + 256 * i, t = idx >> 6, k4 = idx & 63;
@@ -41,8 +42,8 @@ __global__ void __launch_bounds__(256) router_logits_kernel(const float* __restr
                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {                                 // Wr: 256 x 16 floats as float4
-        const int idx = tid + 256 * i, k = idx >> 2, e4 = idx & 3;
+    for (int i = 0; i < 2; ++i) {                                 // Wr: 256 x 8 floats as float4
+        const int idx = tid + 256 * i, k = idx >> 1, e4 = idx & 1;
         wv[i] = *reinterpret_cast<const float4*>(Wr + size_t(kb + k) * E + e0 + 4 * e4);
     }
 #pragma unroll
@@ -51,27 +52,29 @@ __global__ void __launch_bounds__(256) router_logits_kernel(const float* __restr
         *reinterpret_cast<float4*>(xs + t * RXS + 4 * k4) = xv[i];
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int idx = tid + 256 * i, k = idx >> 2, e4 = idx & 3;
-        *reinterpret_cast<float4*>(ws + k * 16 + 4 * e4) = wv[i];
+    for (int i = 0; i < 2; ++i) {
+        const int idx = tid + 256 * i, k = idx >> 1, e4 = idx & 1;
+        ws[(4 * e4 + 0) * RXS + k] = wv[i].x;
+        ws[(4 * e4 + 1) * RXS + k] = wv[i].y;
+        ws[(4 * e4 + 2) * RXS + k] = wv[i].z;
+        ws[(4 * e4 + 3) * RXS + k] = wv[i].w;
     }
     __syncthreads();
-    const int t = tid >> 3, e2 = tid & 7;
-    float acc0 = 0.0f, acc1 = 0.0f;
+    // thread (token t, expert e1): one fma chain over the chunk's k ascending
+    const int t = tid >> 3, e1 = tid & 7;
+    float acc = 0.0f;
     const float* xa = xs + t * RXS;
-#pragma unroll 4
+    const float* wa = ws + e1 * RXS;
+#pragma unroll 8
     for (int k = 0; k < RKW; k += 4) {
         const float4 a = *reinterpret_cast<const float4*>(xa + k);
-        const float av[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float2 w = *reinterpret_cast<const float2*>(ws + (k + j) * 16 + 2 * e2);
-            acc0 = __builtin_fmaf(av[j], w.x, acc0);
-            acc1 = __builtin_fmaf(av[j], w.y, acc1);
-        }
+        const float4 b = *reinterpret_cast<const float4*>(wa + k);
+        acc = __builtin_fmaf(a.x, b.x, acc);
+        acc = __builtin_fmaf(a.y, b.y, acc);
+        acc = __builtin_fmaf(a.z, b.z, acc);
+        acc = __builtin_fmaf(a.w, b.w, acc);
     }
-    if (t0 + t < T)
-        *reinterpret_cast<float2*>(part + (size_t(c) * T + t0 + t) * E + e0 + 2 * e2) = make_float2(acc0, acc1);
+    if (t0 + t < T) part[(size_t(c) * T + t0 + t) * E + e0 + e1] = acc;
     if (q != nullptr && blockIdx.x == 0) {
         // A8 of the slice: (token, group) pair p = tid / 4, 4 threads x 32 values each
         const int p = tid >> 2, part4 = tid & 3, tt = p >> 1, gl = p & 1;
@@ -874,7 +877,7 @@ hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, i
         if (e != hipSuccess) return e;
         attr = true;
     }
-    const dim3 grid(E / 16, (T + 31) / 32, ROUTER_KC);
+    const dim3 grid(E / REW, (T + 31) / 32, ROUTER_KC);
     router_logits_kernel<<<grid, 256, ROUTER_LDS, st>>>(x, Wr, T, H, E, part, q, qs, qsum);
     return hipGetLastError();
 }
