@@ -11,9 +11,9 @@ constexpr int MAXB = 32;    // tokens per routing block (one 32-bit token mask p
 constexpr int MAXE = 256;   // experts (one thread each)
 
 // logits partial c: fma chain over k = c H/8 .. (c+1) H/8 - 1 ascending from 0 (the summation order is fixed so
-// the CPU checker reproduces it). Workgroup tile: 32 tokens x 16 experts of one K chunk, the chunk's x and Wr
-// slices staged in LDS by one batch of loads; thread: 1 token x 2 experts. grid (E/16, ceil(T/32), 8) = 128
-// workgroups at T <= 32, 256 threads, dynamic LDS ROUTER_LDS.
+// the CPU checker reproduces it). Workgroup tile: 32 tokens x 8 experts of one K chunk, the chunk's x slice and
+// its Wr slice (transposed, k contiguous per expert) staged in LDS by one batch of loads; thread: 1 token x 1
+// expert, one chain. grid (E/8, ceil(T/32), 8) = 256 workgroups at T <= 32, 256 threads, dynamic LDS ROUTER_LDS.
 // With q != nullptr the workgroups of expert slice 0 also write the A8 of their x slice (two 128-groups per
 // token, the same operations as quant_a8_kernel), so the layer input is quantised without a launch of its own.
 __device__ __forceinline__ uint32_t okey(float v) {        // order-preserving unsigned image of a float
