@@ -7,14 +7,27 @@ namespace llmoe {
 
 namespace {
 
+// The value of lane (lane ^ o), o a power of two below 64 known at compile time after unrolling: DPP quad
+// permutes for o = 1, 2 (no LDS round trip), ds_swizzle's xor mode inside 32-lane halves for o = 4 .. 16,
+// ds_bpermute for o = 32. The same data movement as __shfl_xor.
+__device__ __forceinline__ int xor_lane(int v, int o) {
+    if (o == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);    // quad_perm [1, 0, 3, 2]
+    if (o == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);    // quad_perm [2, 3, 0, 1]
+    if (o == 4) return __builtin_amdgcn_ds_swizzle(v, (4 << 10) | 0x1F);     // and 0x1F, or 0, xor 4
+    if (o == 8) return __builtin_amdgcn_ds_swizzle(v, (8 << 10) | 0x1F);
+    if (o == 16) return __builtin_amdgcn_ds_swizzle(v, (16 << 10) | 0x1F);
+    return __shfl_xor(v, o);
+}
+__device__ __forceinline__ float xor_lane(float v, int o) { return __int_as_float(xor_lane(__float_as_int(v), o)); }
+
 __device__ __forceinline__ float group16_max(float m) {
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, xor_lane(m, o));
     return m;
 }
 __device__ __forceinline__ int group16_sum(int v) {
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o);
+    for (int o = 1; o < 16; o <<= 1) v += xor_lane(v, o);
     return v;
 }
 __device__ __forceinline__ int clamp127(float r) { return int(fminf(fmaxf(r, -127.0f), 127.0f)); }
@@ -85,7 +98,7 @@ __global__ void __launch_bounds__(256) fwht_a8_kernel(const uint16_t* __restrict
         const bool hi = lane & o;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float y = __shfl_xor(x[j], o);
+            const float y = xor_lane(x[j], o);
             x[j] = hi ? y - x[j] : x[j] + y;
         }
     }
@@ -160,7 +173,7 @@ __device__ __forceinline__ void fwht2048_ab(float (&x)[8], float* v) {
         const bool hi = lane & o;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float y = __shfl_xor(x[j], o);
+            const float y = xor_lane(x[j], o);
             x[j] = hi ? y - x[j] : x[j] + y;
         }
     }
@@ -226,7 +239,7 @@ __global__ void __launch_bounds__(256) combine_norm_kernel(const float* __restri
         p = p + x[j] * x[j];
     }
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) p = p + __shfl_xor(p, o);
+    for (int o = 1; o < 64; o <<= 1) p = p + xor_lane(p, o);
     if (lane == 0) red[i >> 6] = p;
     __syncthreads();
     const float tot = ((red[0] + red[1]) + red[2]) + red[3];
