@@ -128,6 +128,19 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
 constexpr int I2F_BIAS = 0x4B400000;
 __device__ __forceinline__ float biased_to_f32(int c) { return __int_as_float(c) - 12582912.0f; }
 
+// The value of lane (lane ^ o), o a wave-uniform power of two below 64 (all lanes active): DPP quad permutes for
+// o = 1, 2 (no LDS round trip), ds_swizzle's xor mode inside 32-lane halves for o = 4 .. 16, ds_bpermute for
+// o = 32. The same data movement as __shfl_xor.
+__device__ __forceinline__ int xor_lane(int v, int o) {
+    if (o == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);    // quad_perm [1, 0, 3, 2]
+    if (o == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);    // quad_perm [2, 3, 0, 1]
+    if (o == 4) return __builtin_amdgcn_ds_swizzle(v, (4 << 10) | 0x1F);     // and 0x1F, or 0, xor 4
+    if (o == 8) return __builtin_amdgcn_ds_swizzle(v, (8 << 10) | 0x1F);
+    if (o == 16) return __builtin_amdgcn_ds_swizzle(v, (16 << 10) | 0x1F);
+    return __shfl_xor(v, o);
+}
+__device__ __forceinline__ float xor_lane(float v, int o) { return __int_as_float(xor_lane(__float_as_int(v), o)); }
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
 }

@@ -82,8 +82,8 @@ __global__ void __launch_bounds__(256) router_logits_kernel(const float* __restr
         float m = 0.0f;
 #pragma unroll
         for (int j = 0; j < 32; ++j) m = fmaxf(m, fabsf(v[j]));
-        m = fmaxf(m, __shfl_xor(m, 1));
-        m = fmaxf(m, __shfl_xor(m, 2));
+        m = fmaxf(m, xor_lane(m, 1));
+        m = fmaxf(m, xor_lane(m, 2));
         const float sc = fmaxf(m / 127.0f, 1e-30f);
         int tot = 0;
         uint32_t w[8];
@@ -95,8 +95,8 @@ __global__ void __launch_bounds__(256) router_logits_kernel(const float* __restr
             tot += qq;
             w[j >> 2] |= uint32_t(qq & 0xFF) << (8 * (j & 3));
         }
-        tot += __shfl_xor(tot, 1);
-        tot += __shfl_xor(tot, 2);
+        tot += xor_lane(tot, 1);
+        tot += xor_lane(tot, 2);
         if (t0 + tt < T) {
             int8_t* dst = q + size_t(t0 + tt) * H + kb + gl * GROUP + part4 * 32;
             *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
@@ -159,7 +159,7 @@ __device__ __forceinline__ void merge8(uint64_t (&k)[8], const uint64_t (&w)[8])
 }
 
 __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int o) {
-    const uint32_t lo = __shfl_xor(uint32_t(v), o), hi = __shfl_xor(uint32_t(v >> 32), o);
+    const uint32_t lo = uint32_t(xor_lane(int(uint32_t(v)), o)), hi = uint32_t(xor_lane(int(uint32_t(v >> 32)), o));
     return (uint64_t(hi) << 32) | lo;
 }
 
@@ -325,7 +325,7 @@ __global__ void __launch_bounds__(RT_THREADS) route_kernel(const float* __restri
         best[j] = ok ? sel_key(sig[tl][ex] + sbias[ex], ex) : 0ull;
     }
     sort8(best);
-#pragma unroll 1
+#pragma unroll
     for (int o = 1; o < 32; o <<= 1) {
         uint64_t other[8];
 #pragma unroll
