@@ -251,13 +251,6 @@ __global__ void __launch_bounds__(RT_THREADS) route_kernel(const float* __restri
     __shared__ float sbias[MAXE];
     __shared__ int inpool[MAXE];
     __shared__ uint32_t tmask[MAXE];
-    __shared__ int sstart[MAXE];
-    __shared__ int cnt[MAXE];
-    __shared__ int nits[MAXE];
-    __shared__ int ibase[MAXE];
-    __shared__ int tots[2];
-    __shared__ int wcls[MAXE];
-    __shared__ int nu_gu[MAXE], nu_dn[MAXE], ub_gu[MAXE], ub_dn[MAXE], utot[2];
     const int b = blockIdx.x, t0 = b * block, tb = min(block, T - t0), tid = threadIdx.x;
     if (tid < E) {
         sbias[tid] = bias[tid];
@@ -360,10 +353,10 @@ __global__ void __launch_bounds__(RT_THREADS) route_kernel(const float* __restri
     if (tid < E) mask[size_t(b) * E + tid] = tmask[tid];
 }
 
-// ---- decode routing (one routing block, T <= block <= 32): scores, then selection + dispatch ----------------
-// The selection runs in ceil(T/8) workgroups (8 tokens each, 32 lanes per token) instead of one; the last
-// workgroup to finish (a device-scope counter) builds the slots and work units for all tokens. DecodeState is
-// zero when a call starts and the dispatching workgroup leaves it zero again.
+// ---- decode routing (one routing block, T <= block <= 32) ------------------------------------------------------
+// score_kernel (with the pool), select_token_kernel (one token per workgroup), then dispatch_kernel (one
+// workgroup: slots and work units for all tokens). DecodeState is zero when a call starts, and dispatch_kernel
+// leaves it zero again.
 
 // grid T, 256 threads (thread = expert): logit = partials summed in chunk order; sig[t, e] = sigmoid(logit);
 // with the pool, blockmax[e] = max over tokens of the ordered key of sigmoid + bias
