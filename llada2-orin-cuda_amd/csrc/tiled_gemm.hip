@@ -3,16 +3,17 @@
 // :364-383): per 128-group g, P_g = sum code xq - zero Sxq exact in int32, then
 // acc = fma(scale_w scale_x, float(P_g), acc) for g ascending from 0.
 //
-// Work unit: <= TILED_NTOK (64) slots of one expert and a range of row blocks. The workgroup (8 waves; 16 for down) first
-// copies the chunk's int8 activation rows for the WHOLE reduction (64 x K bytes, XOR-swizzled 16-byte chunks so
-// the MFMA operand reads are conflict-free), their scales and sums into LDS, then every wave streams its own
-// tiled_spw(bits) 16-row strips of each row block through registers: each 16x128 weight tile is unpacked once
-// into MFMA A operands and used for all 4 token tiles, and the fp32 accumulators of the (strip, token tile)
-// pairs stay in registers until the fused epilogue. No barrier inside a row block, so the waves (2 per SIMD; 4 for down)
-// drift freely and one wave's MFMAs overlap the other's vector epilogue.
-// Zero points: for 2/3-bit codes the zero is subtracted while unpacking (a v_perm_b32 lookup of c - z), so the
-// MFMA accumulates from 0; 4-bit codes and 8-bit codes (stored c - 128) start the MFMA from the zero term
-// zero * (-Sxq) of the lane's four output rows instead.
+// Work unit: <= TILED_NTOK (64) slots of one expert and a range of row blocks. The workgroup (8 waves; 16 for
+// down) first copies the chunk's int8 activation rows for the WHOLE reduction (64 x K bytes, XOR-swizzled 16-byte
+// chunks so the MFMA operand reads are conflict-free), their scales and sums into LDS, then every wave streams
+// its own tiled_spw 16-row strips of each row block through registers: each 16x128 weight tile is unpacked once
+// into MFMA A operands and used for all 4 token tiles, and the fp32 accumulators of the (strip, token tile) pairs
+// stay in registers until the fused epilogue. No barrier inside a row block, so the waves (2 per SIMD; 4 for
+// down) drift freely and one wave's MFMAs overlap another's vector epilogue.
+// Zero points: for 2/3-bit codes the zero is subtracted while unpacking (a v_perm_b32 lookup of c - z); 4-bit
+// codes and 8-bit codes (stored c - 128) put the zero term zero * (-Sxq) of the lane's four output rows on the
+// MFMA's initial accumulator instead. Either way the accumulator starts from I2F_BIAS, so its bits end as the
+// float 1.5 * 2^23 + P_g and one subtraction gives float(P_g).
 #include <type_traits>
 
 #include "llmoe_internal.h"
