@@ -141,6 +141,25 @@ __device__ __forceinline__ int xor_lane(int v, int o) {
 }
 __device__ __forceinline__ float xor_lane(float v, int o) { return __int_as_float(xor_lane(__float_as_int(v), o)); }
 
+// Inclusive prefix sum over the 64 lanes of a wave (all lanes active): Hillis-Steele inside each 16-lane row by
+// DPP row shifts (lanes shifted in from outside the row add 0), then the totals of rows 0 and 2 added to rows 1
+// and 3 (row_bcast:15), and the total of rows 0-1 added to rows 2-3 (row_bcast:31).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+    int x = int(v);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);   // row_bcast:15 into rows 1, 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);   // row_bcast:31 into rows 2, 3
+    return uint32_t(x);
+}
+__device__ __forceinline__ int wave_incl_scan(int v) { return int(wave_incl_scan(uint32_t(v))); }
+// 64-bit values whose sums carry nothing from bit 31 into bit 32 (fields of 16 bits): the halves scan apart
+__device__ __forceinline__ uint64_t wave_incl_scan(uint64_t v) {
+    return (uint64_t(wave_incl_scan(uint32_t(v >> 32))) << 32) | wave_incl_scan(uint32_t(v));
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
 }

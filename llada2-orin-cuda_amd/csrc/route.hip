@@ -417,16 +417,9 @@ __global__ void __launch_bounds__(256) dispatch_kernel(int T, int E, int K, cons
     uint64_t ig = vg, id = vd;
     {   // three inclusive scans over the 256 threads in one pass: wave shuffles, then the wave totals
         const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int ui = __shfl_up(incl, o);
-            const uint64_t ug = __shfl_up(ig, o), ud = __shfl_up(id, o);
-            if (lane >= o) {
-                incl += ui;
-                ig += ug;
-                id += ud;
-            }
-        }
+        incl = wave_incl_scan(incl);
+        ig = wave_incl_scan(ig);
+        id = wave_incl_scan(id);
         if (lane == 63) {
             wt_i[w] = incl;
             wt_g[w] = ig;
@@ -656,18 +649,11 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     uint64_t s1 = uint64_t(nit * gemm_row_blocks(true, bw)) << (16 * cls);
     uint64_t t0 = uint64_t(nch) << (16 * cls);
     const uint64_t own0 = s0, own1 = s1, ownt = t0;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int a1 = __shfl_up(incl, o), a2 = __shfl_up(inch, o);
-        const uint64_t b0 = __shfl_up(s0, o), b1 = __shfl_up(s1, o), b2 = __shfl_up(t0, o);
-        if (lane >= o) {
-            incl += a1;
-            inch += a2;
-            s0 += b0;
-            s1 += b1;
-            t0 += b2;
-        }
-    }
+    incl = wave_incl_scan(incl);
+    inch = wave_incl_scan(inch);
+    s0 = wave_incl_scan(s0);
+    s1 = wave_incl_scan(s1);
+    t0 = wave_incl_scan(t0);
     if (lane == 63) {
         wt_i[w] = incl;
         wt_c[w] = inch;
@@ -775,14 +761,8 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
         run1 += cost(task_dn[j]);
     }
     int inc0 = run0, inc1 = run1;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int v0 = __shfl_up(inc0, o), v1 = __shfl_up(inc1, o);
-        if (lane >= o) {
-            inc0 += v0;
-            inc1 += v1;
-        }
-    }
+    inc0 = wave_incl_scan(inc0);
+    inc1 = wave_incl_scan(inc1);
     if (lane == 63) {
         wt_i[w] = inc0;
         wt_c[w] = inc1;
