@@ -568,7 +568,7 @@ __global__ void __launch_bounds__(256) select_token_kernel(const float* __restri
         float wsum = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; ++k)
-            if (k < K) wsum = wsum + __shfl(sk, k);
+            if (k < K) wsum = wsum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sk), k));
         if (lane < K) {
             topk[size_t(t) * K + lane] = ex;
             topw[size_t(t) * K + lane] = sk / (wsum + 1e-20f) * rscale;
