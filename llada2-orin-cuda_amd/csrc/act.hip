@@ -122,22 +122,34 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
     int sl[MAX_KK];
 #pragma unroll
     for (int k = 0; k < MAX_KK; ++k) sl[k] = k < kk ? tok_slots[t * K1 + k] : 0;
-    for (int h = threadIdx.x * 4; h < H; h += blockDim.x * 4) {
-        float4 v[MAX_KK];
+    // R float4 columns per thread per pass (a whole 2048-wide row at 256 threads): every load of the pass is in
+    // flight before the ordered sums
+    constexpr int R = 2;
+    for (int hb = threadIdx.x * 4; hb < H; hb += blockDim.x * 4 * R) {
+        float4 v[R][MAX_KK];
 #pragma unroll
-        for (int k = 0; k < MAX_KK; ++k)   // every load in flight before the ordered sum
-            if (k < kk) v[k] = *reinterpret_cast<const float4*>(Y + size_t(sl[k]) * H + h);
-        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int r = 0; r < R; ++r) {
+            const int h = hb + r * blockDim.x * 4;
 #pragma unroll
-        for (int k = 0; k < MAX_KK; ++k) {
-            if (k < kk) {
-                acc.x = acc.x + v[k].x;
-                acc.y = acc.y + v[k].y;
-                acc.z = acc.z + v[k].z;
-                acc.w = acc.w + v[k].w;
-            }
+            for (int k = 0; k < MAX_KK; ++k)
+                if (k < kk && h < H) v[r][k] = *reinterpret_cast<const float4*>(Y + size_t(sl[k]) * H + h);
         }
-        *reinterpret_cast<float4*>(out + size_t(t) * H + h) = acc;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int h = hb + r * blockDim.x * 4;
+            if (h >= H) break;
+            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int k = 0; k < MAX_KK; ++k) {
+                if (k < kk) {
+                    acc.x = acc.x + v[r][k].x;
+                    acc.y = acc.y + v[r][k].y;
+                    acc.z = acc.z + v[r][k].z;
+                    acc.w = acc.w + v[r][k].w;
+                }
+            }
+            *reinterpret_cast<float4*>(out + size_t(t) * H + h) = acc;
+        }
     }
 }
 
