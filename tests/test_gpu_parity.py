@@ -165,6 +165,25 @@ def test_layer_forward_matches_oracle(gpu, T, mix, shared, pool):
     G.close()
 
 
+@pytest.mark.parametrize("E,K,T,pool", [
+    (64, 4, 32, 16),      # decode, pool
+    (128, 6, 32, 256),    # decode, no pool
+    (64, 8, 100, 48),     # several routing blocks, tiled experts
+    (128, 2, 200, 256),
+])
+def test_other_expert_counts(gpu, E, K, T, pool):
+    """The ABI's other shapes (E a multiple of 64 up to 256, top_k <= 8): every stage bit-exact."""
+    say(f"[shape] E={E} K={K} T={T} pool={pool}")
+    L = synth.make_layer(900 + E + K, E=E, mix="mixed", shared=True)
+    G = make_gpu_layer(L, pool, max_tokens=256, K=K)
+    x = synth.make_x(950 + T, T)
+    out = run_layer(G, x, gpu)
+    r = oracle.Layer(L, K=K).forward(x, C=pool)
+    check_full(G, r, T, K, True)
+    assert np.array_equal(out.view(np.uint32), r["out"].view(np.uint32)), "combine not bit-exact"
+    G.close()
+
+
 @pytest.mark.parametrize("kind", ["zipf", "skewed"])
 def test_logits_routing(gpu, kind):
     T = 128
