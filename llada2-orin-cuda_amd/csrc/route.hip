@@ -11,9 +11,9 @@ constexpr int MAXB = 32;    // tokens per routing block (one 32-bit token mask p
 constexpr int MAXE = 256;   // experts (one thread each)
 
 // logits partial c: fma chain over k = c H/8 .. (c+1) H/8 - 1 ascending from 0 (the summation order is fixed so
-// the CPU checker reproduces it). Workgroup tile: 32 tokens x 8 experts of one K chunk, the chunk's x slice and
-// its Wr slice (transposed, k contiguous per expert) staged in LDS by one batch of loads; thread: 1 token x 1
-// expert, one chain. grid (E/8, ceil(T/32), 8) = 256 workgroups at T <= 32, 256 threads, dynamic LDS ROUTER_LDS.
+// the CPU checker reproduces it). Workgroup tile: TT tokens x EW experts of one K chunk, the chunk's x slice and
+// its Wr slice (transposed, k contiguous per expert) staged in LDS by one batch of loads; each thread runs one
+// chain per (token, expert) it owns. grid (E/EW, ceil(T/TT), 8).
 // With q != nullptr the workgroups of expert slice 0 also write the A8 of their x slice (two 128-groups per
 // token, the same operations as quant_a8_kernel), so the layer input is quantised without a launch of its own.
 __device__ __forceinline__ uint32_t okey(float v) {        // order-preserving unsigned image of a float
@@ -22,59 +22,83 @@ __device__ __forceinline__ uint32_t okey(float v) {        // order-preserving u
 }
 
 constexpr int RKW = 256;                                          // K per chunk (H = 2048)
-constexpr int REW = 8;                                            // experts per workgroup
 constexpr int RXS = RKW + 4;                                      // LDS row stride of the x and Wr slices
-constexpr int ROUTER_LDS = (32 + REW) * RXS * 4;
-__global__ void __launch_bounds__(256) router_logits_kernel(const float* __restrict__ x, const float* __restrict__ Wr,
-                                                            int T, int H, int E, float* __restrict__ part,
-                                                            int8_t* __restrict__ q, float* __restrict__ qs,
-                                                            int* __restrict__ qsum) {
+template <int TT, int EW>
+constexpr int router_lds() { return (TT + EW) * RXS * 4; }
+// Tiles: <32 tokens, 8 experts, 256 threads> (one chain per thread: the decode step, latency-bound) and
+// <64 tokens, 64 experts, 512 threads> (2 tokens x 4 experts per thread: x and Wr reloaded 8x less from L2).
+template <int TT, int EW, int NT>
+__global__ void __launch_bounds__(NT) router_logits_kernel(const float* __restrict__ x, const float* __restrict__ Wr,
+                                                           int T, int H, int E, float* __restrict__ part,
+                                                           int8_t* __restrict__ q, float* __restrict__ qs,
+                                                           int* __restrict__ qsum) {
+    constexpr int TPT = TT * EW / NT >= 8 ? 2 : 1, EPT = TT * EW / NT / TPT;   // chains per thread: TPT x EPT
+    constexpr int EG = EW / EPT;                                             // expert groups (threads per token group)
+    constexpr int XV = TT * (RKW / 4) / NT, WV = RKW * (EW / 4) / NT;
+    static_assert(XV * NT == TT * (RKW / 4) && WV * NT == RKW * (EW / 4) && NT >= TT * 8, "router tile");
     extern __shared__ __align__(16) float rl[];
-    float* xs = rl;                       // [32][RXS]
-    float* ws = rl + 32 * RXS;            // [REW][RXS]: Wr slice transposed, k contiguous per expert
-    const int e0 = blockIdx.x * REW, t0 = blockIdx.y * 32, c = blockIdx.z, kb = c * RKW;
+    float* xs = rl;                       // [TT][RXS]
+    float* ws = rl + TT * RXS;            // [EW][RXS]: Wr slice transposed, k contiguous per expert
+    const int e0 = blockIdx.x * EW, t0 = blockIdx.y * TT, c = blockIdx.z, kb = c * RKW;
     const int tid = threadIdx.x;
-    float4 xv[8], wv[2];
+    float4 xv[XV], wv[WV];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {                                 // x: 32 x 256 floats as float4
-        const int idx = tid + 256 * i, t = idx >> 6, k4 = idx & 63;
+    for (int i = 0; i < XV; ++i) {                                // x: TT x 256 floats as float4
+        const int idx = tid + NT * i, t = idx >> 6, k4 = idx & 63;
         xv[i] = t0 + t < T ? *reinterpret_cast<const float4*>(x + size_t(t0 + t) * H + kb + 4 * k4)
                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {                                 // Wr: 256 x 8 floats as float4
-        const int idx = tid + 256 * i, k = idx >> 1, e4 = idx & 1;
+    for (int i = 0; i < WV; ++i) {                                // Wr: 256 x EW floats as float4
+        const int idx = tid + NT * i, k = idx / (EW / 4), e4 = idx % (EW / 4);
         wv[i] = *reinterpret_cast<const float4*>(Wr + size_t(kb + k) * E + e0 + 4 * e4);
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int idx = tid + 256 * i, t = idx >> 6, k4 = idx & 63;
+    for (int i = 0; i < XV; ++i) {
+        const int idx = tid + NT * i, t = idx >> 6, k4 = idx & 63;
         *reinterpret_cast<float4*>(xs + t * RXS + 4 * k4) = xv[i];
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int idx = tid + 256 * i, k = idx >> 1, e4 = idx & 1;
+    for (int i = 0; i < WV; ++i) {
+        const int idx = tid + NT * i, k = idx / (EW / 4), e4 = idx % (EW / 4);
         ws[(4 * e4 + 0) * RXS + k] = wv[i].x;
         ws[(4 * e4 + 1) * RXS + k] = wv[i].y;
         ws[(4 * e4 + 2) * RXS + k] = wv[i].z;
         ws[(4 * e4 + 3) * RXS + k] = wv[i].w;
     }
     __syncthreads();
-    // thread (token t, expert e1): one fma chain over the chunk's k ascending
-    const int t = tid >> 3, e1 = tid & 7;
-    float acc = 0.0f;
-    const float* xa = xs + t * RXS;
-    const float* wa = ws + e1 * RXS;
-#pragma unroll 8
+    // thread (token group tg, expert group eg): tokens tg TPT + i, experts j EG + eg (consecutive rows of the Wr
+    // slice across a wave's lanes: conflict-free), one fma chain each over the chunk's k ascending
+    const int tg = tid / EG, eg = tid % EG;
+    float acc[TPT][EPT];
+#pragma unroll
+    for (int i = 0; i < TPT; ++i)
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) acc[i][j] = 0.0f;
+#pragma unroll 4
     for (int k = 0; k < RKW; k += 4) {
-        const float4 a = *reinterpret_cast<const float4*>(xa + k);
-        const float4 b = *reinterpret_cast<const float4*>(wa + k);
-        acc = __builtin_fmaf(a.x, b.x, acc);
-        acc = __builtin_fmaf(a.y, b.y, acc);
-        acc = __builtin_fmaf(a.z, b.z, acc);
-        acc = __builtin_fmaf(a.w, b.w, acc);
+        float4 a[TPT], b[EPT];
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) a[i] = *reinterpret_cast<const float4*>(xs + (tg * TPT + i) * RXS + k);
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) b[j] = *reinterpret_cast<const float4*>(ws + (j * EG + eg) * RXS + k);
+#pragma unroll
+        for (int i = 0; i < TPT; ++i)
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) {
+                acc[i][j] = __builtin_fmaf(a[i].x, b[j].x, acc[i][j]);
+                acc[i][j] = __builtin_fmaf(a[i].y, b[j].y, acc[i][j]);
+                acc[i][j] = __builtin_fmaf(a[i].z, b[j].z, acc[i][j]);
+                acc[i][j] = __builtin_fmaf(a[i].w, b[j].w, acc[i][j]);
+            }
     }
-    if (t0 + t < T) part[(size_t(c) * T + t0 + t) * E + e0 + e1] = acc;
+#pragma unroll
+    for (int i = 0; i < TPT; ++i) {
+        const int t = t0 + tg * TPT + i;
+        if (t < T)
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) part[(size_t(c) * T + t) * E + e0 + j * EG + eg] = acc[i][j];
+    }
     if (q != nullptr && blockIdx.x == 0) {
         // A8 of the slice: (token, group) pair p = tid / 4, 4 threads x 32 values each
         const int p = tid >> 2, part4 = tid & 3, tt = p >> 1, gl = p & 1;
@@ -845,13 +869,22 @@ hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, i
                                 float* qs, int* qsum, hipStream_t st) {
     static bool attr = false;
     if (!attr) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(router_logits_kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, ROUTER_LDS);
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(router_logits_kernel<32, 8, 256>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, router_lds<32, 8>());
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(router_logits_kernel<64, 64, 512>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, router_lds<64, 64>());
         if (e != hipSuccess) return e;
         attr = true;
     }
-    const dim3 grid(E / REW, (T + 31) / 32, ROUTER_KC);
-    router_logits_kernel<<<grid, 256, ROUTER_LDS, st>>>(x, Wr, T, H, E, part, q, qs, qsum);
+    if (T <= 32) {
+        const dim3 grid(E / 8, 1, ROUTER_KC);
+        router_logits_kernel<32, 8, 256><<<grid, 256, router_lds<32, 8>(), st>>>(x, Wr, T, H, E, part, q, qs, qsum);
+    } else {
+        const dim3 grid(E / 64, (T + 63) / 64, ROUTER_KC);
+        router_logits_kernel<64, 64, 512><<<grid, 512, router_lds<64, 64>(), st>>>(x, Wr, T, H, E, part, q, qs,
+                                                                                   qsum);
+    }
     return hipGetLastError();
 }
 
