@@ -255,6 +255,21 @@ __device__ __forceinline__ void units_shared(Item* list, int u, int r, int E, in
     list[u] = Item{E, T * K + 16 * j, min(16, T - 16 * j), u % r};
 }
 
+// Descending bitonic sort of one key per lane across the 64 lanes of a wave: lane i ends with the i-th largest.
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t k, int lane) {
+#pragma unroll
+    for (int s = 2; s <= 64; s <<= 1)
+#pragma unroll
+        for (int j = s >> 1; j > 0; j >>= 1) {
+            const uint64_t o = shfl_xor64(k, j);
+            // blocks of s lanes alternate direction (all descending at s = 64); the lower lane of a pair keeps
+            // the larger key in a descending block
+            const bool keep_max = ((lane & j) == 0) == ((lane & s) == 0);
+            k = keep_max ? (o > k ? o : k) : (o < k ? o : k);
+        }
+    return k;
+}
+
 constexpr int RT_THREADS = 1024;
 
 // One routing block per workgroup (engine/ops.cu:256-327, quant/s03_teacher_pass.py:132-146):
@@ -313,20 +328,31 @@ __global__ void __launch_bounds__(RT_THREADS) route_kernel(const float* __restri
         }
     }
     __syncthreads();
-    if (C < E) {
+    // pool = the C largest keys: rank = number of larger keys, counted by binary search in the four waves' sorted
+    // lists of the 256 keys
+    uint64_t ke = 0ull;
+    if (C < E && tid < MAXE) {   // waves 0-3 whole
         if (tid < E) {
             float km = -__builtin_inff();
             for (int t = 0; t < tb; ++t) km = fmaxf(km, sig[t][tid] + sbias[tid]);
-            key[tid] = sel_key(km, tid);
+            ke = sel_key(km, tid);
         }
-        __syncthreads();
+        key[tid] = wave_sort_desc(ke, tid & 63);
     }
-    if (tid < E) {   // pool = the C largest keys: rank = number of larger keys
+    __syncthreads();
+    if (tid < E) {
         int rank = 0;
         if (C < E) {
-            const uint64_t ke = key[tid];
-#pragma unroll 8
-            for (int j = 0; j < E; ++j) rank += key[j] > ke;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint64_t* a = key + v * 64;
+                int lo = 0;
+#pragma unroll
+                for (int step = 32; step > 0; step >>= 1)
+                    if (a[lo + step - 1] > ke) lo += step;
+                if (lo == 63 && a[63] > ke) lo = 64;
+                rank += lo;
+            }
         }
         inpool[tid] = rank < C;
     }
@@ -513,20 +539,6 @@ __global__ void __launch_bounds__(256) dispatch_kernel(int T, int E, int K, cons
     }
 }
 
-// Descending bitonic sort of one key per lane across the 64 lanes of a wave: lane i ends with the i-th largest.
-__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t k, int lane) {
-#pragma unroll
-    for (int s = 2; s <= 64; s <<= 1)
-#pragma unroll
-        for (int j = s >> 1; j > 0; j >>= 1) {
-            const uint64_t o = shfl_xor64(k, j);
-            // blocks of s lanes alternate direction (all descending at s = 64); the lower lane of a pair keeps
-            // the larger key in a descending block
-            const bool keep_max = ((lane & j) == 0) == ((lane & s) == 0);
-            k = keep_max ? (o > k ? o : k) : (o < k ? o : k);
-        }
-    return k;
-}
 
 // Decode selection, one token per workgroup (engine/ops.cu:256-327): thread e scores expert e, each wave sorts
 // its 64 keys, wave 0 sorts the four waves' leaders and writes the top-K, the routing weights
