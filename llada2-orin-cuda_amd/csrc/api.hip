@@ -178,7 +178,7 @@ int plan_and_place(llmoe_layer* L, const int32_t* topk, const float* topw, int T
     HIPCHECK(launch_plan(L->mask, T, d.n_experts, d.top_k, d.block, d.has_shared, L->ntok, L->tiled ? 1 : 0,
                          L->bits_d, L->count, L->start, L->bpre, L->units_gu, L->units_dn, L->tunits_gu,
                          L->tunits_dn, L->n_units, L->g_gu, L->g_dn, L->tstart, int(L->chunks_cap), st));
-    HIPCHECK(launch_place(topk, topw, L->mask, L->bpre, T, d.n_experts, d.top_k, d.block, d.has_shared,
+    HIPCHECK(launch_place(topk, topw, L->mask, L->blockmax, L->bpre, T, d.n_experts, d.top_k, d.block, d.has_shared,
                           L->slot_token, L->slot_weight, L->tok_slots, st));
     L->mark(LLMOE_STAGE_DISPATCH, true, st);
     L->routed_T = T;
@@ -287,11 +287,14 @@ int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t bl
     ALLOC(L->topw, Tm * K);
     ALLOC(L->mask, nbm * E);
     ALLOC(L->bpre, nbm * E);
-    ALLOC(L->sig, size_t(d.block) * E);
-    ALLOC(L->blockmax, E);
+    ALLOC(L->sig, std::max<size_t>(Tm, size_t(d.block)) * E);
+    // token masks and per-block pool maxima are accumulated by atomics: zero here, and left zero again by the
+    // kernel that consumes them (place_kernel, dispatch_kernel)
+    ALLOC(L->blockmax, nbm * E);
     ALLOC(L->tmask, E);
 
-    if (hipMemset(L->blockmax, 0, E * sizeof(uint32_t)) != hipSuccess ||
+    if (hipMemset(L->blockmax, 0, nbm * E * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(L->mask, 0, nbm * E * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(L->tmask, 0, E * sizeof(uint32_t)) != hipSuccess || 
         hipDeviceSynchronize() != hipSuccess)
         return bail(fail(LLMOE_EHIP, "workspace initialisation"));
@@ -371,8 +374,8 @@ int route_impl(llmoe_layer* L, const float* x, const float* logits, int T, hipSt
         L->routed_T = T;
         return LLMOE_OK;
     }
-    HIPCHECK(launch_route(part, nchunks, L->bias, T, d.n_experts, d.top_k, d.pool, d.block, d.routed_scale, L->topk,
-                          L->topw, L->mask, st));
+    HIPCHECK(launch_route(part, nchunks, L->bias, T, d.n_experts, d.top_k, d.pool, d.block, d.routed_scale, L->sig,
+                          L->blockmax, L->topk, L->topw, L->mask, st));
     L->mark(LLMOE_STAGE_ROUTE, true, st);
     return plan_and_place(L, L->topk, L->topw, T, st);
 }

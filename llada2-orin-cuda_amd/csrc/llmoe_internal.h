@@ -216,7 +216,8 @@ hipError_t launch_combine(const float* Y, const int* tok_slots, int T, int H, in
 hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, int E, float* part, int8_t* q,
                                 float* qs, int* qsum, hipStream_t st);
 hipError_t launch_route(const float* part, int nchunks, const float* bias, int T, int E, int K, int C, int block,
-                        float rscale, int32_t* topk, float* topw, uint32_t* mask, hipStream_t st);
+                        float rscale, float* sig, uint32_t* blockmax, int32_t* topk, float* topw, uint32_t* mask,
+                        hipStream_t st);
 // decode step (T <= 32, one routing block): [scores and pool keys (pool < E)], selection in ceil(T/8)
 // workgroups, then one workgroup builds the slots and work units (streamed, 16 slots per item). blockmax / tmask
 // [E] must be zero on entry and are zero again on exit. sig: [T, E] scratch.
@@ -235,8 +236,8 @@ hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int
                        const int8_t* bits, int32_t* count, int32_t* start, int32_t* bpre, Item* units_gu,
                        Item* units_dn, Item* tunits_gu, Item* tunits_dn, int* n_units, int g_gu, int g_dn,
                        int* tstart, int max_chunks, hipStream_t st);
-hipError_t launch_place(const int32_t* topk, const float* topw, const uint32_t* mask, const int32_t* bpre, int T,
-                        int E, int K, int block, int has_shared, int32_t* slot_token, float* slot_weight,
-                        int32_t* tok_slots, hipStream_t st);
+hipError_t launch_place(const int32_t* topk, const float* topw, uint32_t* mask, uint32_t* blockmax,
+                        const int32_t* bpre, int T, int E, int K, int block, int has_shared, int32_t* slot_token,
+                        float* slot_weight, int32_t* tok_slots, hipStream_t st);
 
 }  // namespace llmoe

@@ -134,8 +134,6 @@ __global__ void __launch_bounds__(NT) router_logits_kernel(const float* __restri
     }
 }
 
-__device__ __forceinline__ bool beats(float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); }
-
 // Selection keys: (value desc, index asc) as one unsigned 64-bit order: the float's bits mapped to an
 // order-preserving unsigned integer in the high word, 0xFFFF - index in the low word; key 0 = no candidate.
 __device__ __forceinline__ uint64_t sel_key(float v, int idx) {
@@ -145,42 +143,8 @@ __device__ __forceinline__ uint64_t sel_key(float v, int idx) {
 }
 __device__ __forceinline__ int key_index(uint64_t k) { return 0xFFFF - int(uint32_t(k) & 0xFFFFu); }
 
-__device__ __forceinline__ void cas(uint64_t (&k)[8], int i, int l) {   // afterwards k[i] >= k[l]
-    const uint64_t a = k[i], b = k[l];
-    const bool sw = b > a;
-    k[i] = sw ? b : a;
-    k[l] = sw ? a : b;
-}
 
-// bitonic sorting network on 8 keys, largest first
-__device__ __forceinline__ void sort8(uint64_t (&k)[8]) {
-#pragma unroll
-    for (int s = 2; s <= 8; s <<= 1)
-#pragma unroll
-        for (int j = s >> 1; j > 0; j >>= 1)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int l = i ^ j;
-                if (l > i) {
-                    if ((i & s) == 0) cas(k, i, l);
-                    else cas(k, l, i);
-                }
-            }
-}
 
-// k <- largest 8 of two largest-first sorted lists: max(k[i], w[7 - i]) is bitonic and holds them; a 3-stage
-// bitonic merge sorts it
-__device__ __forceinline__ void merge8(uint64_t (&k)[8], const uint64_t (&w)[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) k[i] = w[7 - i] > k[i] ? w[7 - i] : k[i];
-#pragma unroll
-    for (int j = 4; j > 0; j >>= 1)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int l = i ^ j;
-            if (l > i) cas(k, i, l);
-        }
-}
 
 __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int o) {
     const uint32_t lo = uint32_t(xor_lane(int(uint32_t(v)), o)), hi = uint32_t(xor_lane(int(uint32_t(v >> 32)), o));
@@ -270,138 +234,7 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t k, int lane) {
     return k;
 }
 
-constexpr int RT_THREADS = 1024;
 
-// One routing block per workgroup (engine/ops.cu:256-327, quant/s03_teacher_pass.py:132-146):
-//   logit = sum of the nchunks partials (c ascending); score = sigmoid(logit); s = score + bias;
-//   pool = top-C experts by max over the block's tokens of s, ranked (value desc, index asc) (C >= E: all);
-//   per token top-K of s in the pool, (value desc, index asc): 32 lanes per token each keep a sorted top-8 of
-//   their 8 experts, then five xor-shuffle merges give every lane the token's top-8;
-//   w_k = score_k / (sum_k score_k + 1e-20) * rscale, the sum in rank order.
-// Writes topk/topw [T, K] and mask[block, e] = bit t of the block's tokens that picked e (the multi-block path;
-// the decode step uses score / select / dispatch below). 1024 threads: every partial of the block is loaded in
-// one batch.
-__global__ void __launch_bounds__(RT_THREADS) route_kernel(const float* __restrict__ part, int nchunks,
-                                                           const float* __restrict__ bias, int T, int E, int K, int C,
-                                                           int block, float rscale, int* __restrict__ topk,
-                                                           float* __restrict__ topw, uint32_t* __restrict__ mask) {
-    __shared__ float sig[MAXB][MAXE + 1];
-    __shared__ uint64_t key[MAXE];
-    __shared__ float sbias[MAXE];
-    __shared__ int inpool[MAXE];
-    __shared__ uint32_t tmask[MAXE];
-    const int b = blockIdx.x, t0 = b * block, tb = min(block, T - t0), tid = threadIdx.x;
-    if (tid < E) {
-        sbias[tid] = bias[tid];
-        tmask[tid] = 0u;
-    }
-    {   // logits: positions (token, 4 experts), <= 2 per thread, all chunks loaded before any is summed
-        const int E4 = E / 4, npos = tb * E4;
-        float4 p[2][ROUTER_KC];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int pos = tid + r * RT_THREADS, t = pos / E4, e4 = pos % E4;
-#pragma unroll
-            for (int c = 0; c < ROUTER_KC; ++c)
-                if (pos < npos && c < nchunks)
-                    p[r][c] = *reinterpret_cast<const float4*>(part + (size_t(c) * T + t0 + t) * E + 4 * e4);
-        }
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int pos = tid + r * RT_THREADS, t = pos / E4, e4 = pos % E4;
-            if (pos < npos) {
-                float4 l = p[r][0];
-#pragma unroll
-                for (int c = 1; c < ROUTER_KC; ++c) {
-                    if (c < nchunks) {
-                        l.x = l.x + p[r][c].x;
-                        l.y = l.y + p[r][c].y;
-                        l.z = l.z + p[r][c].z;
-                        l.w = l.w + p[r][c].w;
-                    }
-                }
-                sig[t][4 * e4] = sigmoid_f32(l.x);
-                sig[t][4 * e4 + 1] = sigmoid_f32(l.y);
-                sig[t][4 * e4 + 2] = sigmoid_f32(l.z);
-                sig[t][4 * e4 + 3] = sigmoid_f32(l.w);
-            }
-        }
-    }
-    __syncthreads();
-    // pool = the C largest keys: rank = number of larger keys, counted by binary search in the four waves' sorted
-    // lists of the 256 keys
-    uint64_t ke = 0ull;
-    if (C < E && tid < MAXE) {   // waves 0-3 whole
-        if (tid < E) {
-            float km = -__builtin_inff();
-            for (int t = 0; t < tb; ++t) km = fmaxf(km, sig[t][tid] + sbias[tid]);
-            ke = sel_key(km, tid);
-        }
-        key[tid] = wave_sort_desc(ke, tid & 63);
-    }
-    __syncthreads();
-    if (tid < E) {
-        int rank = 0;
-        if (C < E) {
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const uint64_t* a = key + v * 64;
-                int lo = 0;
-#pragma unroll
-                for (int step = 32; step > 0; step >>= 1)
-                    if (a[lo + step - 1] > ke) lo += step;
-                if (lo == 63 && a[63] > ke) lo = 64;
-                rank += lo;
-            }
-        }
-        inpool[tid] = rank < C;
-    }
-    __syncthreads();
-    // selection: 32 lanes per token (all 1024 threads), 8 candidates per lane read before use and sorted, then
-    // five xor-shuffle merges (1 .. 16) give every lane of the token its best 8
-    const int tl = tid >> 5, sub = tid & 31;
-    uint64_t best[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int ex = sub * 8 + j;
-        const bool ok = tl < tb && ex < E && inpool[ex];
-        best[j] = ok ? sel_key(sig[tl][ex] + sbias[ex], ex) : 0ull;
-    }
-    sort8(best);
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) {
-        uint64_t other[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) other[k] = shfl_xor64(best[k], o);
-        merge8(best, other);
-    }
-    int bi[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) bi[k] = key_index(best[k]);
-    float mine = 0.0f, wsum = 0.0f;
-    int mysel = 0;
-    const bool owner = tl < tb && sub < K;
-    if (tl < tb) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if (k < K) {
-                const float sk = sig[tl][bi[k]];
-                wsum = wsum + sk;
-                if (k == sub) {
-                    mine = sk;
-                    mysel = bi[k];
-                }
-            }
-        }
-        if (owner) {
-            topk[size_t(t0 + tl) * K + sub] = mysel;
-            topw[size_t(t0 + tl) * K + sub] = mine / (wsum + 1e-20f) * rscale;
-            atomicOr(&tmask[mysel], 1u << tl);
-        }
-    }
-    __syncthreads();
-    if (tid < E) mask[size_t(b) * E + tid] = tmask[tid];
-}
 
 // ---- decode routing (one routing block, T <= block <= 32) ------------------------------------------------------
 // score_kernel (with the pool), select_token_kernel (one token per workgroup), then dispatch_kernel (one
@@ -411,8 +244,9 @@ __global__ void __launch_bounds__(RT_THREADS) route_kernel(const float* __restri
 // grid T, 256 threads (thread = expert): logit = partials summed in chunk order; sig[t, e] = sigmoid(logit);
 // with the pool, blockmax[e] = max over tokens of the ordered key of sigmoid + bias
 __global__ void __launch_bounds__(256) score_kernel(const float* __restrict__ part, int nchunks,
-                                                    const float* __restrict__ bias, int T, int E, int pool_on,
-                                                    float* __restrict__ sig, uint32_t* __restrict__ blockmax) {
+                                                    const float* __restrict__ bias, int T, int E, int block,
+                                                    int pool_on, float* __restrict__ sig,
+                                                    uint32_t* __restrict__ blockmax) {
     const int t = blockIdx.x, e = threadIdx.x;
     if (e >= E) return;
     float p[ROUTER_KC];
@@ -424,7 +258,7 @@ __global__ void __launch_bounds__(256) score_kernel(const float* __restrict__ pa
         if (c < nchunks) l = l + p[c];
     const float sg = sigmoid_f32(l);
     sig[size_t(t) * E + e] = sg;
-    if (pool_on) atomicMax(&blockmax[e], okey(sg + bias[e]));
+    if (pool_on) atomicMax(&blockmax[size_t(t / block) * E + e], okey(sg + bias[e]));
 }
 
 struct DecodeState {
@@ -551,7 +385,7 @@ template <bool POOL>
 __global__ void __launch_bounds__(256) select_token_kernel(const float* __restrict__ part, int nchunks,
                                                            const float* __restrict__ sig,
                                                            const float* __restrict__ bias, int T, int E, int K,
-                                                           int C, float rscale, int* __restrict__ topk,
+                                                           int C, int block, float rscale, int* __restrict__ topk,
                                                            float* __restrict__ topw, DecodeState ds) {
     __shared__ float sig_s[MAXE];
     __shared__ uint64_t lead[4 * 8];
@@ -559,7 +393,8 @@ __global__ void __launch_bounds__(256) select_token_kernel(const float* __restri
     const int t = blockIdx.x, e = threadIdx.x, lane = e & 63, w = e >> 6;
     bool inpool = true;
     if constexpr (POOL) {
-        const uint64_t pk = e < E ? (uint64_t(ds.blockmax[e]) << 32) | uint32_t(0xFFFF - e) : 0ull;
+        const uint64_t pk =
+            e < E ? (uint64_t(ds.blockmax[size_t(t / block) * E + e]) << 32) | uint32_t(0xFFFF - e) : 0ull;
         pool_s[w * 64 + lane] = wave_sort_desc(pk, lane);
         __syncthreads();
         int rank = 0;
@@ -608,7 +443,7 @@ __global__ void __launch_bounds__(256) select_token_kernel(const float* __restri
         if (lane < K) {
             topk[size_t(t) * K + lane] = ex;
             topw[size_t(t) * K + lane] = sk / (wsum + 1e-20f) * rscale;
-            atomicOr(&ds.tmask[ex], 1u << t);
+            atomicOr(&ds.tmask[size_t(t / block) * E + ex], 1u << (t % block));
         }
     }
 }
@@ -851,8 +686,9 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
 
 // Place every (token, k) pair in its slot; tok_slots[t, K] = the shared slot (or -1). grid nb, 256 threads.
 __global__ void __launch_bounds__(256) place_kernel(const int* __restrict__ topk, const float* __restrict__ topw,
-                                                    const uint32_t* __restrict__ mask, const int* __restrict__ bpre,
-                                                    int T, int E, int K, int block, int has_shared,
+                                                    uint32_t* __restrict__ mask, uint32_t* __restrict__ blockmax,
+                                                    const int* __restrict__ bpre, int T, int E, int K, int block,
+                                                    int has_shared,
                                                     int* __restrict__ slot_token, float* __restrict__ slot_weight,
                                                     int* __restrict__ tok_slots) {
     const int b = blockIdx.x, t0 = b * block, tb = min(block, T - t0);
@@ -872,6 +708,12 @@ __global__ void __launch_bounds__(256) place_kernel(const int* __restrict__ topk
             slot_weight[T * K + t] = 1.0f;
         }
         tok_slots[size_t(t) * (K + 1) + K] = has_shared ? T * K + t : -1;
+    }
+    // the block's token masks and pool maxima are consumed: leave them zero for the next call's atomics
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        mask[size_t(b) * E + e] = 0u;
+        blockmax[size_t(b) * E + e] = 0u;
     }
 }
 
@@ -901,9 +743,18 @@ hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, i
 }
 
 hipError_t launch_route(const float* part, int nchunks, const float* bias, int T, int E, int K, int C, int block,
-                        float rscale, int32_t* topk, float* topw, uint32_t* mask, hipStream_t st) {
-    const int nb = (T + block - 1) / block;
-    route_kernel<<<nb, RT_THREADS, 0, st>>>(part, nchunks, bias, T, E, K, C, block, rscale, topk, topw, mask);
+                        float rscale, float* sig, uint32_t* blockmax, int32_t* topk, float* topw, uint32_t* mask,
+                        hipStream_t st) {
+    if (E > MAXE || block > MAXB) return hipErrorInvalidValue;
+    const DecodeState ds{blockmax, mask};
+    if (C < E) {
+        score_kernel<<<T, 256, 0, st>>>(part, nchunks, bias, T, E, block, 1, sig, blockmax);
+        select_token_kernel<true><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, block, rscale, topk,
+                                                      topw, ds);
+    } else {
+        select_token_kernel<false><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, block, rscale, topk,
+                                                       topw, ds);
+    }
     return hipGetLastError();
 }
 
@@ -915,10 +766,12 @@ hipError_t launch_decode_route(const float* part, int nchunks, const float* bias
     if (T > 32 || E > MAXE) return hipErrorInvalidValue;
     const DecodeState ds{blockmax, tmask};
     if (C < E) {
-        score_kernel<<<T, 256, 0, st>>>(part, nchunks, bias, T, E, 1, sig, blockmax);
-        select_token_kernel<true><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, rscale, topk, topw, ds);
+        score_kernel<<<T, 256, 0, st>>>(part, nchunks, bias, T, E, MAXB, 1, sig, blockmax);
+        select_token_kernel<true><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, MAXB, rscale, topk, topw,
+                                                      ds);
     } else {
-        select_token_kernel<false><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, rscale, topk, topw, ds);
+        select_token_kernel<false><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, MAXB, rscale, topk, topw,
+                                                       ds);
     }
     const DispatchOut d{has_shared, 16, bits, count, start, units_gu, units_dn, n_units, slot_token, slot_weight,
                         tok_slots};
@@ -943,12 +796,12 @@ hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int
     return hipGetLastError();
 }
 
-hipError_t launch_place(const int32_t* topk, const float* topw, const uint32_t* mask, const int32_t* bpre, int T,
-                        int E, int K, int block, int has_shared, int32_t* slot_token, float* slot_weight,
-                        int32_t* tok_slots, hipStream_t st) {
+hipError_t launch_place(const int32_t* topk, const float* topw, uint32_t* mask, uint32_t* blockmax,
+                        const int32_t* bpre, int T, int E, int K, int block, int has_shared, int32_t* slot_token,
+                        float* slot_weight, int32_t* tok_slots, hipStream_t st) {
     const int nb = (T + block - 1) / block;
-    place_kernel<<<nb, 256, 0, st>>>(topk, topw, mask, bpre, T, E, K, block, has_shared, slot_token, slot_weight,
-                                     tok_slots);
+    place_kernel<<<nb, 256, 0, st>>>(topk, topw, mask, blockmax, bpre, T, E, K, block, has_shared, slot_token,
+                                     slot_weight, tok_slots);
     return hipGetLastError();
 }
 
