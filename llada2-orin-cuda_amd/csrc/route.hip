@@ -657,7 +657,9 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     }
     __syncthreads();
     PLAN_TRACE(3);
-    // work partition: chunk j hands workgroup w (lo_w = ceil(w C / G) in [pre_j, pre_j+1)) its first task
+    // work partition: workgroup q starts at task position lo_q = ceil(q C / G); the chunk j holding it
+    // (pre[j] <= lo_q < pre[j + 1]) is found by binary search, and the task inside it is the first row block
+    // whose cost span starts at or after lo_q (one past the chunk's last: the next chunk's first)
     for (int m = 0; m < 2; ++m) {
         const int G = m ? g_dn : g_gu;
         const int* P = m ? pre_dn : pre_gu;
@@ -665,20 +667,21 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
         int* ts = tstart + (m ? g_gu + 1 : 0);
         const long long C = P[n];
         if (e == 0) ts[G] = n;
-        if (C == 0) {
-            for (int q = e; q < G; q += blockDim.x) ts[q] = n;
-            continue;
-        }
-        // workgroups past the last task start (lo_w >= C, possible when C < G) get none
-        for (long long q = floor_div((C - 1) * G, C) + 1 + e; q < G; q += blockDim.x) ts[q] = n;
-        for (int j = e; j < n; j += blockDim.x) {
-            const int p0 = P[j], p1 = P[j + 1], nrb = int(task[j] & 255u), span = int(task[j] >> 8);
-            for (long long q = p0 == 0 ? 0 : floor_div((long long)(p0 - 1) * G, C) + 1; q < G; ++q) {
-                const long long lo = floor_div(q * C + G - 1, G);
-                if (lo >= p1) break;
-                const int r = int((lo - p0 + span - 1) / span);
-                ts[q] = r >= nrb ? j + 1 : (j | (r << TASK_RB_SHIFT));
+        for (int q = e; q < G; q += blockDim.x) {
+            const long long lo = C == 0 ? 0 : floor_div((long long)q * C + G - 1, G);
+            if (lo >= C) {
+                ts[q] = n;
+                continue;
             }
+            int a = 0, b = n;   // P[a] <= lo < P[b]
+            while (b - a > 1) {
+                const int mid = (a + b) >> 1;
+                if (P[mid] <= lo) a = mid;
+                else b = mid;
+            }
+            const int nrb = int(task[a] & 255u), span = int(task[a] >> 8);
+            const int r = int((lo - P[a] + span - 1) / span);
+            ts[q] = r >= nrb ? a + 1 : (a | (r << TASK_RB_SHIFT));
         }
     }
     PLAN_TRACE(4);
