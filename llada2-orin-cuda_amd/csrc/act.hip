@@ -82,12 +82,11 @@ __global__ void __launch_bounds__(256) fwht_a8_kernel(const uint16_t* __restrict
             }
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const bool hi = lane & o;
+        // butterfly: the lower lane of the pair keeps x + y, the upper y - x; fma(+-1, x, y) rounds exactly
+        // like that sum or difference
+        const float sg = (lane & o) ? -1.0f : 1.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float y = xor_lane(x[j], o);
-            x[j] = hi ? y - x[j] : x[j] + y;
-        }
+        for (int j = 0; j < 8; ++j) x[j] = __builtin_fmaf(sg, x[j], xor_lane(x[j], o));
     }
     float m = 0.0f;
 #pragma unroll
@@ -169,12 +168,11 @@ __device__ __forceinline__ void fwht2048_ab(float (&x)[8], float* v) {
             }
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const bool hi = lane & o;
+        // butterfly: the lower lane of the pair keeps x + y, the upper y - x; fma(+-1, x, y) rounds exactly
+        // like that sum or difference
+        const float sg = (lane & o) ? -1.0f : 1.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float y = xor_lane(x[j], o);
-            x[j] = hi ? y - x[j] : x[j] + y;
-        }
+        for (int j = 0; j < 8; ++j) x[j] = __builtin_fmaf(sg, x[j], xor_lane(x[j], o));
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[8 * i + j] = x[j];
