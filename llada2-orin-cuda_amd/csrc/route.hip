@@ -99,7 +99,7 @@ __global__ void __launch_bounds__(NT) router_logits_kernel(const float* __restri
 #pragma unroll
             for (int j = 0; j < EPT; ++j) part[(size_t(c) * T + t) * E + e0 + j * EG + eg] = acc[i][j];
     }
-    if (q != nullptr && blockIdx.x == 0) {
+    if (q != nullptr && blockIdx.x == 0 && tid < TT * 8) {
         // A8 of the slice: (token, group) pair p = tid / 4, 4 threads x 32 values each
         const int p = tid >> 2, part4 = tid & 3, tt = p >> 1, gl = p & 1;
         const float* v = xs + tt * RXS + gl * GROUP + part4 * 32;
