@@ -81,10 +81,9 @@ __device__ __forceinline__ float pow2i(int k) { return __int_as_float((k + 127) 
 
 // exp(x): Cody-Waite reduction with ln2 = hi + lo (hi has 12 trailing zero bits), Taylor polynomial of degree 7
 // on |r| <= ln2/2, scaling by 2^n as two exact power-of-two factors.
-__device__ __forceinline__ float exp_f32(float x) {
-    if (x != x) return x;
-    if (x > 88.72283935546875f) return __builtin_inff();
-    if (x < -103.97208404541016f) return 0.0f;
+// exp's polynomial path (Cody-Waite reduction with ln2 = hi + lo, hi with 12 trailing zero bits; Taylor
+// polynomial of degree 7; the 2^n scaling split in two so that n down to -150 stays exact)
+__device__ __forceinline__ float exp_poly(float x) {
     const float n = __builtin_rintf(x * 1.44269502162933349609375f);
     float r = __builtin_fmaf(n, -0.693145751953125f, x);
     r = __builtin_fmaf(n, -1.428606765330187045037746429443359375e-06f, r);
@@ -99,6 +98,17 @@ __device__ __forceinline__ float exp_f32(float x) {
     const int ni = int(n), e1 = ni / 2, e2 = ni - e1;
     return (p * pow2i(e1)) * pow2i(e2);
 }
+__device__ __forceinline__ float exp_f32(float x) {
+    // when every active lane is inside the polynomial's range (the common case) the special cases are skipped;
+    // otherwise the polynomial runs on x clamped into the range and the special results are selected. Either
+    // way the values equal those of the early-return form of the CPU checker.
+    const bool in = x >= -103.97208404541016f && x <= 88.72283935546875f;   // false for nan
+    if (__all(in)) return exp_poly(x);
+    float v = exp_poly(fminf(fmaxf(x, -103.97208404541016f), 88.72283935546875f));
+    v = x > 88.72283935546875f ? __builtin_inff() : v;
+    v = x < -103.97208404541016f ? 0.0f : v;
+    return x != x ? x : v;
+}
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + exp_f32(-x)); }
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + exp_f32(-x)); }
 
@@ -107,21 +117,20 @@ __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + exp_f32(
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     const uint32_t x = __float_as_uint(f);
     const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
-    uint32_t h;
-    if (ax >= 0x7f800000u) {
-        h = 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u);              // inf / nan
-    } else if (ax >= 0x477ff000u) {
-        h = 0x7c00u;                                                  // >= 65520 rounds to inf
-    } else if (ax < 0x38800000u) {
-        h = uint32_t(__builtin_rintf(__uint_as_float(ax) * 16777216.0f));   // subnormal half: exact scale by 2^24
-    } else {
-        const uint32_t mant = ax & 0x7fffffu;
-        h = ((((ax >> 23) - 112u)) << 10) | (mant >> 13);
-        const uint32_t rem = mant & 0x1fffu;
-        h += (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ? 1u : 0u;
-    }
+    const uint32_t mant = ax & 0x7fffffu, rem = mant & 0x1fffu;
+    uint32_t hn = (((ax >> 23) - 112u) << 10) | (mant >> 13);                      // normal half
+    hn += (rem > 0x1000u || (rem == 0x1000u && (hn & 1u))) ? 1u : 0u;
+    // every active lane a normal half (the common case): done; otherwise every range's result is computed and
+    // the one for ax selected
+    if (__all(ax - 0x38800000u < 0x477ff000u - 0x38800000u)) return uint16_t(sign | hn);
+    // subnormal half: exact scale by 2^24 (the operand clamped so that no lane converts an inf or nan)
+    const uint32_t hs = uint32_t(__builtin_rintf(__uint_as_float(ax < 0x38800000u ? ax : 0x38800000u) * 16777216.0f));
+    uint32_t h = ax < 0x38800000u ? hs : hn;
+    h = ax >= 0x477ff000u ? 0x7c00u : h;                                          // >= 65520 rounds to inf
+    h = ax >= 0x7f800000u ? (0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u)) : h;    // inf / nan
     return uint16_t(sign | h);
 }
+
 // int32 -> fp32 through the MFMA accumulator: a product that starts from I2F_BIAS (the bits of 1.5 * 2^23) ends as
 // the bits of the float 1.5 * 2^23 + P exactly when |P| < 2^22 (every group product: |c - z| <= 255, |xq| <= 127,
 // 128 terms), so one subtraction -- cheaper than v_cvt_f32_i32 on gfx950 -- returns float(P) exactly.
