@@ -493,6 +493,8 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     PLAN_TRACE(0);
     // token masks: unconditional loads at clamped indices, so that each batch is issued back to back
     const int ec = min(e, E - 1);
+    // code widths read up front, with the masks: a load after them would expose its own latency
+    const int bw_ld = bits[ec], sbits_ld = has_shared ? bits[E] : 8;
     uint32_t mv[NBR];
 #pragma unroll
     for (int j = 0; j < NBR; ++j) mv[j] = mask[size_t(min(j, nb - 1)) * E + ec];
@@ -511,7 +513,7 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     const bool big = e < E && tiled && c > 0;
     const bool sbig = has_shared && tiled;
     const int nsch = sbig ? tiled_chunks(T) : 0;
-    const int bw = e < E ? bits[e] : 2, cls = width_class(bw);
+    const int bw = e < E ? bw_ld : 2, cls = width_class(bw);
     const int nit = e < E && !big ? (c + ntok - 1) / ntok : 0, nch = big ? tiled_chunks(c) : 0;
     // one pass of inclusive scans over the experts: slots, tiled chunks, and per width class (16-bit fields) the
     // streamed units of both lists and the tiled chunks
@@ -547,7 +549,7 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
         wt_i[0] = inch;            // all routed chunks (read after the barrier below)
     }
     __syncthreads();
-    const int sbits = has_shared ? bits[E] : 8;
+    const int sbits = sbits_ld;
     const int ns = has_shared && !sbig ? (T + ntok - 1) / ntok : 0;
     // offsets: the shared expert's units first, then width classes 0 .. 3 (8, 4, 3, 2 bits), expert ascending
     int bg = ns * gemm_row_blocks(false, sbits), bd = ns * gemm_row_blocks(true, sbits), bt = nsch;
