@@ -696,12 +696,20 @@ __global__ void __launch_bounds__(256) place_kernel(const int* __restrict__ topk
                                                     int has_shared,
                                                     int* __restrict__ slot_token, float* __restrict__ slot_weight,
                                                     int* __restrict__ tok_slots) {
+    // the block's masks and slot bases staged in LDS while the (token, k) pairs load, so the slot of a pair
+    // costs one global round trip
+    __shared__ uint32_t m_s[MAXE];
+    __shared__ int bp_s[MAXE];
     const int b = blockIdx.x, t0 = b * block, tb = min(block, T - t0);
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        m_s[e] = mask[size_t(b) * E + e];
+        bp_s[e] = bpre[size_t(b) * E + e];
+    }
+    __syncthreads();
     for (int p = threadIdx.x; p < tb * K; p += blockDim.x) {
         const int tl = p / K, k = p % K, t = t0 + tl;
         const int ex = topk[size_t(t) * K + k];
-        const uint32_t m = mask[size_t(b) * E + ex];
-        const int sl = bpre[size_t(b) * E + ex] + __popc(m & ((1u << tl) - 1u));
+        const int sl = bp_s[ex] + __popc(m_s[ex] & ((1u << tl) - 1u));
         slot_token[sl] = t;
         slot_weight[sl] = topw[size_t(t) * K + k];
         tok_slots[size_t(t) * (K + 1) + k] = sl;
