@@ -159,6 +159,16 @@ void choose_items(llmoe_layer* L, int T) {
     L->tiled = T > d.block && T > TILED_MIN;   // the single-block decode routing emits streamed units only
 }
 
+// work-item capacity for T tokens, checked before any kernel of the call is launched: the routing kernels OR
+// bits into the layer's token masks and pool maxima, which only the placement kernel clears again
+int prepare_items(llmoe_layer* L, int T) {
+    choose_items(L, T);
+    if (size_t(L->max_items) > L->items_cap)
+        return fail(LLMOE_EINVAL, "item capacity exceeded (%d items for T = %d, capacity %zu)", L->max_items, T,
+                    L->items_cap);
+    return LLMOE_OK;
+}
+
 int check_T(const llmoe_layer* L, int T) {
     if (T < 1 || T > L->d.max_tokens) return fail(LLMOE_EINVAL, "T = %d outside [1, max_tokens = %d]", T, L->d.max_tokens);
     return LLMOE_OK;
@@ -172,8 +182,6 @@ hipError_t launch_gemm(int mode, const GemmArgs& g, const GemmArgs& tg, bool til
 
 int plan_and_place(llmoe_layer* L, const int32_t* topk, const float* topw, int T, hipStream_t st) {
     const auto& d = L->d;
-    choose_items(L, T);
-    if (size_t(L->max_items) > L->items_cap) return fail(LLMOE_EINVAL, "item capacity exceeded");
     L->mark(LLMOE_STAGE_DISPATCH, false, st);
     HIPCHECK(launch_plan(L->mask, T, d.n_experts, d.top_k, d.block, d.has_shared, L->ntok, L->tiled ? 1 : 0,
                          L->bits_d, L->count, L->start, L->bpre, L->units_gu, L->units_dn, L->tunits_gu,
@@ -351,6 +359,7 @@ namespace {
 int route_impl(llmoe_layer* L, const float* x, const float* logits, int T, hipStream_t st, bool quant) {
     const auto& d = L->d;
     L->routed_T = -1;
+    if (int rc = prepare_items(L, T)) return rc;
     const float* part = logits;
     int nchunks = 1;
     if (x) {
@@ -364,8 +373,6 @@ int route_impl(llmoe_layer* L, const float* x, const float* logits, int T, hipSt
     }
     L->mark(LLMOE_STAGE_ROUTE, false, st);
     if (T <= d.block) {   // one routing block (a decode step): route, plan and place in one workgroup
-        choose_items(L, T);
-        if (size_t(L->max_items) > L->items_cap) return fail(LLMOE_EINVAL, "item capacity exceeded");
         HIPCHECK(launch_decode_route(part, nchunks, L->bias, T, d.n_experts, d.top_k, d.pool, d.routed_scale, L->sig,
                                      L->topk, L->topw, L->blockmax, L->tmask, d.has_shared, L->bits_d,
                                      L->count, L->start, L->units_gu, L->units_dn, L->n_units, L->slot_token,
@@ -397,6 +404,7 @@ int llmoe_dispatch(llmoe_layer* L, const int32_t* topk, const float* topw, int T
     const auto& d = L->d;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     L->routed_T = -1;
+    if (int rc = prepare_items(L, T)) return rc;
     HIPCHECK(hipMemcpyAsync(L->topk, topk, size_t(T) * d.top_k * sizeof(int32_t), hipMemcpyDeviceToDevice, st));
     HIPCHECK(hipMemcpyAsync(L->topw, topw, size_t(T) * d.top_k * sizeof(float), hipMemcpyDeviceToDevice, st));
     HIPCHECK(launch_masks(L->topk, T, d.n_experts, d.top_k, d.block, L->mask, st));

@@ -517,19 +517,17 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     const int nit = e < E && !big ? (c + ntok - 1) / ntok : 0, nch = big ? tiled_chunks(c) : 0;
     // one pass of inclusive scans over the experts: slots, tiled chunks, and per width class (16-bit fields) the
     // streamed units of both lists and the tiled chunks
-    int incl = c, inch = nch;
+    int incl = c;
     uint64_t s0 = uint64_t(nit * gemm_row_blocks(false, bw)) << (16 * cls);
     uint64_t s1 = uint64_t(nit * gemm_row_blocks(true, bw)) << (16 * cls);
     uint64_t t0 = uint64_t(nch) << (16 * cls);
     const uint64_t own0 = s0, own1 = s1, ownt = t0;
     incl = wave_incl_scan(incl);
-    inch = wave_incl_scan(inch);
     s0 = wave_incl_scan(s0);
     s1 = wave_incl_scan(s1);
     t0 = wave_incl_scan(t0);
     if (lane == 63) {
         wt_i[w] = incl;
-        wt_c[w] = inch;
         wt[w][0] = s0;
         wt[w][1] = s1;
         wt[w][2] = t0;
@@ -537,7 +535,6 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     __syncthreads();
     for (int i = 0; i < w; ++i) {
         incl += wt_i[i];
-        inch += wt_c[i];
         s0 += wt[i][0];
         s1 += wt[i][1];
         t0 += wt[i][2];
@@ -546,7 +543,6 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
         tot[0] = s0;
         tot[1] = s1;
         tot[2] = t0;
-        wt_i[0] = inch;            // all routed chunks (read after the barrier below)
     }
     __syncthreads();
     const int sbits = sbits_ld;
