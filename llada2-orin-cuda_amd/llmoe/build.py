@@ -27,16 +27,36 @@ HIPCC_FLAGS = [
 
 
 def build_library(verbose: bool = False) -> Path:
+    """Each source compiled to an object in parallel (separate code objects, no device-side linking), then linked."""
+    from concurrent.futures import ThreadPoolExecutor
+
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
     out = PKG / "libllmoe.so"
     tmp = out.with_suffix(".so.tmp")
-    cmd = [hipcc, *HIPCC_FLAGS, f"-I{ROOT / 'include'}", f"-I{CSRC}", *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
-    r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+    objdir = PKG / "_build"
+    objdir.mkdir(exist_ok=True)
+    inc = [f"-I{ROOT / 'include'}", f"-I{CSRC}"]
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+
+    def compile_one(src: str):
+        obj = objdir / (src + ".o")
+        cmd = [hipcc, *compile_flags, *inc, "-c", str(CSRC / src), "-o", str(obj)]
+        return src, obj, subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+
+    jobs = max(1, min(len(SOURCES), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
+    with ThreadPoolExecutor(jobs) as ex:
+        results = list(ex.map(compile_one, SOURCES))
+    for src, _, r in results:
+        if r.returncode != 0:
+            sys.stderr.write(r.stdout + r.stderr)
+            raise RuntimeError(f"hipcc failed on {src}")
+        if verbose:
+            sys.stderr.write(r.stderr)
+    r = subprocess.run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *[str(o) for _, o, _ in results], "-o",
+                        str(tmp)], capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError("hipcc failed building libllmoe.so")
-    if verbose:
-        sys.stderr.write(r.stderr)
+        raise RuntimeError("linking libllmoe.so failed")
     os.replace(tmp, out)
     return out
 
