@@ -105,6 +105,20 @@ int llmoe_experts_norm(llmoe_layer* layer, const int8_t* xq, const float* xs, co
                        const float* signs, float eps, float* h, int8_t* q_next, float* s_next, int32_t* sum_next,
                        llmoe_stream stream);
 
+/* llmoe_experts without any device memory of the layer's own for the expert stage's intermediates (Z, its A8,
+ * the slot outputs Y): they live in one static device array per GPU, LLMOE_SCRATCH_BYTES bytes, held by each GPU
+ * the library runs on until the process ends. No counterpart in the reference: for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc) and for stacks of layers
+ * that share one set of intermediates. The call allocates nothing and performs no memset; nothing in the array
+ * needs to start at zero (every element a call reads was written earlier in that call). T <= LLMOE_SCRATCH_MAX_TOKENS
+ * (larger T: LLMOE_EINVAL); hidden 2048, inter 512, top_k <= 8. Every call on one GPU shares the array: calls that
+ * overlap on one GPU (other streams, other threads) race and must be serialised by the caller. Same results as
+ * llmoe_experts. */
+#define LLMOE_SCRATCH_MAX_TOKENS 64
+#define LLMOE_SCRATCH_BYTES 5621760u
+int llmoe_experts_scratch(llmoe_layer* layer, const int8_t* xq, const float* xs, const int32_t* xsum, int T,
+                          float* out, llmoe_stream stream);
+
 /* Whole layer: A8(x) -> route (x Wr, or the given logits) -> experts -> out. x fp32 [T, H]. */
 int llmoe_layer_forward(llmoe_layer* layer, const float* x, const float* logits, int T, float* out,
                         llmoe_stream stream);

@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <set>
 #include <string>
@@ -70,6 +71,14 @@ struct NormOut {            // the combine's fused epilogue (llmoe_experts_norm)
     int32_t* sum;
 };
 
+struct Inter {              // the expert stage's intermediates between the kernels
+    uint16_t* Z;            // fp16 SiLU(g) u                 [S, I]
+    int8_t* zq;             // A8(Z H512)                     [S, I]
+    float* zs;              //                                [S, I / 128]
+    int32_t* zsum;          //                                [S, I / 128]
+    float* Y;               // weighted expert outputs        [S, H]
+};
+
 struct llmoe_layer {
     llmoe_layer_desc d{};
     int nexp = 0;                                   // E + has_shared
@@ -111,6 +120,7 @@ struct llmoe_layer {
     GemmArgs last_gu{}, last_dn{}, last_tgu{}, last_tdn{};
     float* last_out = nullptr;
     NormOut last_norm{};
+    Inter last_w{};
     int last_S = 0, last_T = 0, last_nt = 1;
     bool last_tiled = false;
     bool have_last = false;
@@ -414,8 +424,10 @@ int llmoe_dispatch(llmoe_layer* L, const int32_t* topk, const float* topw, int T
 }  // extern "C"
 
 namespace {
+Inter layer_inter(const llmoe_layer* L) { return Inter{L->Z, L->zq, L->zs, L->zsum, L->Y}; }
+
 int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_t* xsum, int T, float* out,
-                 const NormOut& no, hipStream_t st) {
+                 const NormOut& no, const Inter& w, hipStream_t st) {
     if (T != L->routed_T) return fail(LLMOE_ESTATE, "no routing for T = %d (route or dispatch first)", T);
     const auto& d = L->d;
     const int H = d.hidden, I = d.inter, K = d.top_k;
@@ -430,7 +442,7 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     g.off = L->gu_off_d;
     g.slot_token = L->slot_token;
     g.xq = xq; g.xs = xs; g.xsum = xsum;
-    g.K = H; g.R = 2 * I; g.Z = L->Z;
+    g.K = H; g.R = 2 * I; g.Z = w.Z;
     GemmArgs tg = g;
     tg.items = L->tunits_gu;
     tg.tstart = L->tstart;
@@ -441,31 +453,32 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     HIPCHECK(launch_gemm(GEMM_GATE_UP, g, tg, L->tiled, st));
     L->mark(LLMOE_STAGE_GATE_UP, true, st);
     L->mark(LLMOE_STAGE_FWHT, false, st);
-    HIPCHECK(launch_fwht_a8(L->Z, S, L->zq, L->zs, L->zsum, st));
+    HIPCHECK(launch_fwht_a8(w.Z, S, w.zq, w.zs, w.zsum, st));
     L->mark(LLMOE_STAGE_FWHT, true, st);
     // down: B rows are slot rows of Z'
     g.items = L->units_dn;
     g.n_items = L->n_units + 1;
     g.off = L->d_off_d;
     g.slot_token = nullptr;
-    g.xq = L->zq; g.xs = L->zs; g.xsum = L->zsum;
-    g.K = I; g.R = H; g.Z = nullptr; g.Y = L->Y;
+    g.xq = w.zq; g.xs = w.zs; g.xsum = w.zsum;
+    g.K = I; g.R = H; g.Z = nullptr; g.Y = w.Y;
     tg = g;
     tg.items = L->tunits_dn;
     tg.tstart = L->tstart + L->g_gu + 1;
     tg.n_items = L->n_units + 3;
     L->last_dn = g;
     L->last_tdn = tg;
-    L->last_S = S; L->last_T = T; L->last_tiled = L->tiled; L->last_out = out; L->last_norm = no; L->have_last = true;
+    L->last_S = S; L->last_T = T; L->last_tiled = L->tiled; L->last_out = out; L->last_norm = no; L->last_w = w;
+    L->have_last = true;
     L->mark(LLMOE_STAGE_DOWN, false, st);
     HIPCHECK(launch_gemm(GEMM_DOWN, g, tg, L->tiled, st));
     L->mark(LLMOE_STAGE_DOWN, true, st);
     L->mark(LLMOE_STAGE_COMBINE, false, st);
     if (no.h)
-        HIPCHECK(launch_combine_norm(L->Y, L->tok_slots, T, K + (d.has_shared ? 1 : 0), K + 1, no.signs, no.eps, no.h,
+        HIPCHECK(launch_combine_norm(w.Y, L->tok_slots, T, K + (d.has_shared ? 1 : 0), K + 1, no.signs, no.eps, no.h,
                                      no.q, no.s, no.sum, st));
     else
-        HIPCHECK(launch_combine(L->Y, L->tok_slots, T, H, K + (d.has_shared ? 1 : 0), K + 1, out, st));
+        HIPCHECK(launch_combine(w.Y, L->tok_slots, T, H, K + (d.has_shared ? 1 : 0), K + 1, out, st));
     L->mark(LLMOE_STAGE_COMBINE, true, st);
     return LLMOE_OK;
 }
@@ -477,7 +490,7 @@ int llmoe_experts(llmoe_layer* L, const int8_t* xq, const float* xs, const int32
                   llmoe_stream stream) {
     if (int rc = check_layer(L)) return rc;
     if (!xq || !xs || !xsum || !out) return fail(LLMOE_EINVAL, "null argument");
-    return experts_impl(L, xq, xs, xsum, T, out, NormOut{}, static_cast<hipStream_t>(stream));
+    return experts_impl(L, xq, xs, xsum, T, out, NormOut{}, layer_inter(L), static_cast<hipStream_t>(stream));
 }
 
 int llmoe_experts_norm(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_t* xsum, int T,
@@ -489,7 +502,64 @@ int llmoe_experts_norm(llmoe_layer* L, const int8_t* xq, const float* xs, const 
     if (L->d.hidden != 2048) return fail(LLMOE_EINVAL, "the rotation is FWHT-2048: hidden must be 2048");
     if (L->d.top_k + (L->d.has_shared ? 1 : 0) > 9) return fail(LLMOE_EINVAL, "at most 9 slots per token");
     return experts_impl(L, xq, xs, xsum, T, nullptr, NormOut{signs, eps, h, q_next, s_next, sum_next},
-                        static_cast<hipStream_t>(stream));
+                        layer_inter(L), static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+namespace {
+// Intermediates of llmoe_experts_scratch: one file-scope device array per GPU, sized for LLMOE_SCRATCH_MAX_TOKENS
+// tokens of K <= 8 routed slots plus the shared slot. Regions (256-byte aligned): Z fp16 [S, 512], zq int8 [S, 512],
+// zs fp32 [S, 4], zsum int32 [S, 4], Y fp32 [S, 2048].
+constexpr size_t SCR_S = size_t(LLMOE_SCRATCH_MAX_TOKENS) * 9;
+constexpr size_t SCR_Z = 0;
+constexpr size_t SCR_ZQ = SCR_Z + SCR_S * 512 * 2;
+constexpr size_t SCR_ZS = SCR_ZQ + SCR_S * 512;
+constexpr size_t SCR_ZSUM = SCR_ZS + SCR_S * 4 * 4;
+constexpr size_t SCR_Y = SCR_ZSUM + SCR_S * 4 * 4;
+constexpr size_t SCR_BYTES = SCR_Y + SCR_S * 2048 * 4;
+static_assert(SCR_ZQ % 256 == 0 && SCR_ZS % 256 == 0 && SCR_ZSUM % 256 == 0 && SCR_Y % 256 == 0, "alignment");
+static_assert(SCR_BYTES == LLMOE_SCRATCH_BYTES, "LLMOE_SCRATCH_BYTES in llmoe.h");
+
+static __device__ __align__(256) uint8_t scratch[SCR_BYTES];
+
+constexpr int SCR_MAX_DEV = 64;
+std::mutex g_scr_mu;
+uint8_t* g_scr_ptr[SCR_MAX_DEV] = {};   // device address of `scratch` on each GPU (the host symbol is a stand-in)
+
+int scratch_ptr(uint8_t** out) {
+    int dev = 0;
+    HIPCHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= SCR_MAX_DEV) return fail(LLMOE_EINVAL, "device %d beyond the scratch table", dev);
+    std::lock_guard<std::mutex> lk(g_scr_mu);
+    if (!g_scr_ptr[dev]) {
+        void* p = nullptr;
+        HIPCHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(LLMOE_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+        g_scr_ptr[dev] = static_cast<uint8_t*>(p);
+    }
+    *out = g_scr_ptr[dev];
+    return LLMOE_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int llmoe_experts_scratch(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_t* xsum, int T, float* out,
+                          llmoe_stream stream) {
+    if (int rc = check_layer(L)) return rc;
+    if (!xq || !xs || !xsum || !out) return fail(LLMOE_EINVAL, "null argument");
+    if (T < 1 || T > LLMOE_SCRATCH_MAX_TOKENS)
+        return fail(LLMOE_EINVAL, "T = %d outside [1, %d] (the static scratch of llmoe_experts_scratch)", T,
+                    LLMOE_SCRATCH_MAX_TOKENS);
+    if (L->d.hidden != 2048 || L->d.inter != 512 || L->d.top_k > 8)
+        return fail(LLMOE_EINVAL, "the static scratch is sized for hidden 2048, inter 512, top_k <= 8");
+    uint8_t* base = nullptr;
+    if (int rc = scratch_ptr(&base)) return rc;
+    const Inter w{reinterpret_cast<uint16_t*>(base + SCR_Z), reinterpret_cast<int8_t*>(base + SCR_ZQ),
+                  reinterpret_cast<float*>(base + SCR_ZS), reinterpret_cast<int32_t*>(base + SCR_ZSUM),
+                  reinterpret_cast<float*>(base + SCR_Y)};
+    return experts_impl(L, xq, xs, xsum, T, out, NormOut{}, w, static_cast<hipStream_t>(stream));
 }
 
 int llmoe_layer_forward(llmoe_layer* L, const float* x, const float* logits, int T, float* out, llmoe_stream stream) {
@@ -536,13 +606,13 @@ hipError_t relaunch_stage(llmoe_layer* L, int stage, hipStream_t st) {
     switch (stage) {
         case LLMOE_STAGE_GATE_UP: return launch_gemm(GEMM_GATE_UP, L->last_gu, L->last_tgu, L->last_tiled, st);
         case LLMOE_STAGE_DOWN: return launch_gemm(GEMM_DOWN, L->last_dn, L->last_tdn, L->last_tiled, st);
-        case LLMOE_STAGE_FWHT: return launch_fwht_a8(L->Z, L->last_S, L->zq, L->zs, L->zsum, st);
+        case LLMOE_STAGE_FWHT: return launch_fwht_a8(L->last_w.Z, L->last_S, L->last_w.zq, L->last_w.zs, L->last_w.zsum, st);
         case LLMOE_STAGE_COMBINE:
             if (L->last_norm.h)   // re-adds into h: each repeat moves the residual stream on by one more layer
-                return launch_combine_norm(L->Y, L->tok_slots, L->last_T, d.top_k + (d.has_shared ? 1 : 0),
+                return launch_combine_norm(L->last_w.Y, L->tok_slots, L->last_T, d.top_k + (d.has_shared ? 1 : 0),
                                            d.top_k + 1, L->last_norm.signs, L->last_norm.eps, L->last_norm.h,
                                            L->last_norm.q, L->last_norm.s, L->last_norm.sum, st);
-            return launch_combine(L->Y, L->tok_slots, L->last_T, d.hidden, d.top_k + (d.has_shared ? 1 : 0),
+            return launch_combine(L->last_w.Y, L->tok_slots, L->last_T, d.hidden, d.top_k + (d.has_shared ? 1 : 0),
                                   d.top_k + 1, L->last_out, st);
         default: return hipErrorInvalidValue;
     }

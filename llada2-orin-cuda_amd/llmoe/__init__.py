@@ -20,6 +20,7 @@ _HERE = Path(__file__).resolve().parent
 LIB_PATH = _HERE / "libllmoe.so"
 
 LLMOE_OK = 0
+SCRATCH_MAX_TOKENS = 64   # LLMOE_SCRATCH_MAX_TOKENS of include/llmoe.h
 LLMOE_EINVAL = -1   # bad argument or shape
 LLMOE_ENOMEM = -2
 LLMOE_EHIP = -3
@@ -64,7 +65,7 @@ EXPORTS = [
     "llmoe_experts", "llmoe_experts_norm", "llmoe_layer_forward", "llmoe_layer_buffers", "llmoe_layer_weight_bytes",
     "llmoe_group_products", "llmoe_layer_set_profiling", "llmoe_layer_stage_ms", "llmoe_layer_time_stage", "llmoe_layers_time_stage",
     "llmoe_layer_load", "llmoe_model_signs", "llmoe_dense_create", "llmoe_dense_destroy", "llmoe_dense_forward",
-    "llmoe_last_error",
+    "llmoe_last_error", "llmoe_experts_scratch",
 ]
 
 STAGES = ["quant", "router", "route", "dispatch", "gate_up", "fwht", "down", "combine"]
@@ -95,6 +96,7 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.llmoe_route.argtypes = [vp, vp, vp, i, vp]
     lib.llmoe_dispatch.argtypes = [vp, vp, vp, i, vp]
     lib.llmoe_experts.argtypes = [vp, vp, vp, vp, i, vp, vp]
+    lib.llmoe_experts_scratch.argtypes = [vp, vp, vp, vp, i, vp, vp]
     lib.llmoe_experts_norm.argtypes = [vp, vp, vp, vp, i, vp, f, vp, vp, vp, vp, vp]
     lib.llmoe_layer_forward.argtypes = [vp, vp, vp, i, vp, vp]
     lib.llmoe_layer_buffers.argtypes = [vp, ctypes.POINTER(Buffers)]
@@ -203,6 +205,16 @@ class Layer:
         if out is None:
             out = torch.empty((T, self.desc.hidden), dtype=torch.float32, device=xq.device)
         _check(self.lib.llmoe_experts(self.handle, _ptr(xq), _ptr(xs), _ptr(xsum), T, _ptr(out), _stream(stream)))
+        return out
+
+    def experts_scratch(self, xq, xs, xsum, out=None, stream=None):
+        """llmoe_experts with the intermediates in the library's static per-GPU scratch (T <= 64)."""
+        import torch
+        T = xq.shape[0]
+        if out is None:
+            out = torch.empty((T, self.desc.hidden), dtype=torch.float32, device=xq.device)
+        _check(self.lib.llmoe_experts_scratch(self.handle, _ptr(xq), _ptr(xs), _ptr(xsum), T, _ptr(out),
+                                              _stream(stream)))
         return out
 
     def experts_norm(self, xq, xs, xsum, signs, eps, h, out=None, stream=None):
