@@ -146,6 +146,19 @@ def norm_step(llmoe, torch, Gs, x, steps, warmup):
             "combine_ms": llmoe.time_stage_layers(Gs, "combine", 20)}
 
 
+def spot_check(L, out_rows, x_rows, lg_rows, pool):
+    """One routing block of a timed configuration against the CPU oracle, outside the timed region: the block's
+    routing depends on its own tokens only, so the oracle runs on those rows alone."""
+    import oracle
+    r = oracle.Layer(L).forward(np.ascontiguousarray(x_rows), logits=None if lg_rows is None else
+                                np.ascontiguousarray(lg_rows), C=pool)
+    err = float(np.abs(out_rows - r["out"]).max()) / max(float(np.abs(r["out"]).max()), 1e-30)
+    exact = bool(np.array_equal(out_rows.view(np.uint32), r["out"].view(np.uint32)))
+    if not exact:
+        log(f"[bench] WARNING: spot check differs from the oracle (max rel err {err:.3e})")
+    return {"rows": f"0-{out_rows.shape[0] - 1}", "bit_exact": exact, "max_abs_err_rel": err}
+
+
 def stack_config(llmoe, synth, torch, steps, warmup, nlayers=20, T=2048):
     """Config 3: 2048 tokens through 20 independently seeded mixed-bit layers (+ shared), Zipf(1.1) load."""
     dev = torch.device("cuda:0")
@@ -156,9 +169,11 @@ def stack_config(llmoe, synth, torch, steps, warmup, nlayers=20, T=2048):
         L = synth.make_layer(1000 + li, mix="mixed", shared=True, zero_bias=True)
         layers.append((L, make_gpu_layer(llmoe, L, 256, T)))
         logits.append(torch.from_numpy(synth.logits_zipf(2000 + li, T)).to(dev))
-        del L["blob"]
+        if li:
+            del L["blob"]
     log(f"[bench] config 3: {nlayers} layers built in {time.perf_counter() - t0:.1f} s")
-    x = torch.from_numpy(synth.make_x(7, T)).to(dev)
+    x_np = synth.make_x(7, T)
+    x = torch.from_numpy(x_np).to(dev)
     out = torch.empty((T, H), dtype=torch.float32, device=dev)
 
     def fn(i):
@@ -172,6 +187,10 @@ def stack_config(llmoe, synth, torch, steps, warmup, nlayers=20, T=2048):
         topk = G.read("topk", (T, K), np.int32)
         wbytes += gate_up_bytes(L, topk) + down_bytes(L, topk)
     Gs = [G for _, G in layers]
+    L0, G0 = layers[0]
+    G0.forward(x, logits[0], out=out)
+    torch.cuda.synchronize()
+    check = spot_check(L0, out[:32].cpu().numpy(), x_np[:32], logits[0][:32].cpu().numpy(), 256)
     gu = llmoe.time_stage_layers(Gs, "gate_up", 3)
     dn = llmoe.time_stage_layers(Gs, "down", 3)
     gu_ms, dn_ms = [gu] * nlayers, [dn] * nlayers
@@ -186,6 +205,7 @@ def stack_config(llmoe, synth, torch, steps, warmup, nlayers=20, T=2048):
         "int8_TOPS": 2 * slots * 3 * I * H / t_w / 1e12,
         "int8_mfma_frac_peak": 2 * slots * 3 * I * H / t_w / 1e12 / PEAK_INT8_TOPS,
         "gate_up_ms_per_layer": float(np.mean(gu_ms)), "down_ms_per_layer": float(np.mean(dn_ms)),
+        "spot_check_layer0": check,
     }
     for _, G in layers:
         G.close()
@@ -226,7 +246,8 @@ def prefill_config(llmoe, synth, torch, name, T, mix, shared, pool, logits_kind,
     Ls = [synth.make_layer(300 + 7 * i, mix=mix, shared=shared, zero_bias=logits_kind is not None)
           for i in range(nlayers)]
     Gs = [make_gpu_layer(llmoe, L, pool, T) for L in Ls]
-    x = torch.from_numpy(synth.make_x(31, T, outlier_frac=outliers)).to(dev)
+    x_np = synth.make_x(31, T, outlier_frac=outliers)
+    x = torch.from_numpy(x_np).to(dev)
     lgs = [None] * nlayers
     if logits_kind == "uniform":
         lgs = [torch.from_numpy(np.random.default_rng(40 + i).standard_normal((T, E)).astype(np.float32)).to(dev)
@@ -236,6 +257,10 @@ def prefill_config(llmoe, synth, torch, name, T, mix, shared, pool, logits_kind,
     out = torch.empty((T, H), dtype=torch.float32, device=dev)
     fn = lambda i: Gs[i % nlayers].forward(x, lgs[i % nlayers], out=out)  # noqa: E731
     dt = time_steps(fn, steps, warmup)
+    fn(0)
+    torch.cuda.synchronize()
+    check = spot_check(Ls[0], out[:32].cpu().numpy(), x_np[:32], None if lgs[0] is None else lgs[0][:32].cpu().numpy(),
+                       pool)
     for i in range(nlayers):
         fn(i)
     gu = llmoe.time_stage_layers(Gs, "gate_up", 5)
@@ -250,7 +275,8 @@ def prefill_config(llmoe, synth, torch, name, T, mix, shared, pool, logits_kind,
             "gate_up_ms": gu, "down_ms": dn, "weight_bytes": wb, "weight_stream_GBps": wb / t_w / 1e9,
             "weight_stream_frac_peak": wb / t_w / 1e9 / PEAK_HBM_GBS,
             "int8_TOPS": 2 * slots * 3 * I * H / t_w / 1e12,
-            "int8_mfma_frac_peak": 2 * slots * 3 * I * H / t_w / 1e12 / PEAK_INT8_TOPS}
+            "int8_mfma_frac_peak": 2 * slots * 3 * I * H / t_w / 1e12 / PEAK_INT8_TOPS, "layers_cycled": nlayers,
+            "spot_check_layer0": check}
 
 
 def dense_config(llmoe, synth, torch, R, bits, T, steps, warmup, nmat=40):
@@ -273,9 +299,34 @@ def dense_config(llmoe, synth, torch, R, bits, T, steps, warmup, nmat=40):
             "int8_mfma_frac_peak": 2 * T * R * H / t / 1e12 / PEAK_INT8_TOPS}
 
 
+def cpu_threads():
+    return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+
+def cpu_baseline_2048(synth, seconds):
+    """The CPU oracle on one config-3 layer (2048 tokens, mixed bits + shared, Zipf(1.1) logits): whole passes until
+    `seconds` have elapsed (at least one)."""
+    import oracle
+    threads = cpu_threads()
+    L = synth.make_layer(1000, mix="mixed", shared=True, zero_bias=True)
+    x = synth.make_x(7, 2048)
+    lg = synth.logits_zipf(2000, 2048)
+    O = oracle.Layer(L)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.forward(x, logits=lg, C=256, nthreads=threads)
+        n += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": 2048 * n / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n} full pass(es) of one config-3 layer (2048 tokens, Zipf(1.1) logits) through the C oracle, "
+                      f"{dt:.1f} s"}
+
+
 def cpu_baseline(L, x_np, pool, seconds):
     import oracle
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    threads = cpu_threads()
     O = oracle.Layer(L)
     T = x_np.shape[0]
     n, t0 = 0, time.perf_counter()
@@ -300,6 +351,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-headline", action="store_true", help="config 1 only (profiling runs)")
     ap.add_argument("--only-stack", action="store_true", help="config 3 only (profiling runs of the tiled GEMM)")
+    ap.add_argument("--only", choices=["config2", "config4-2", "config4-4", "config4-8"],
+                    help="one prefill configuration only, printed as its own JSON line (profiling runs)")
     ap.add_argument("--copy-calibration", action="store_true", help="run 512 MiB device copies first (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -316,6 +369,17 @@ def main():
     if args.copy_calibration:
         copy_calibration(torch)
 
+    if args.only:
+        if args.only == "config2":
+            r = prefill_config(llmoe, synth, torch, "config 2", 512, "mixed", True, 48, None, max(2, args.steps // 10), 2,
+                               nlayers=4, outliers=0.01)
+        else:
+            bits = int(args.only[-1])
+            r = [prefill_config(llmoe, synth, torch, f"config 4: {bits}-bit {kind}", 4096, bits, False, 256, kind,
+                                max(2, args.steps // 40), 1, nlayers=1 if bits == 8 else 2)
+                 for kind in ("uniform", "skewed")]
+        print(json.dumps(r))
+        return
     if args.only_stack:
         print(json.dumps(stack_config(llmoe, synth, torch, max(1, args.steps // 20), max(1, args.warmup // 10))))
         return
@@ -336,7 +400,7 @@ def main():
         log("[bench] config 2")
         configs.append(prefill_config(llmoe, synth, torch, "config 2: 512 tokens, mixed 2/3/4-bit + W8A8 shared, "
                                       "router x Wr with 1% outlier channels x20, block pool 48", 512, "mixed", True,
-                                      48, None, max(2, args.steps // 10), 2, outliers=0.01))
+                                      48, None, max(2, args.steps // 10), 2, nlayers=4, outliers=0.01))
         log("[bench] config 3")
         configs.append(stack_config(llmoe, synth, torch, max(1, args.steps // 20), max(1, args.warmup // 10)))
         for T in (32, 2048):
@@ -360,6 +424,9 @@ def main():
     if not args.no_cpu:
         log("[bench] cpu baseline")
         cpu = cpu_baseline(L1, x1.cpu().numpy(), 256, args.cpu_seconds)
+        if not args.only_headline:
+            log("[bench] cpu baseline, 2048 tokens")
+            cpu["at_2048_tokens"] = cpu_baseline_2048(synth, args.cpu_seconds)
     for G in G1s:
         G.close()
     line = {

@@ -421,9 +421,6 @@ __global__ void __launch_bounds__(nthreads_for(MODE == GEMM_DOWN ? 512 : 2048)) 
 #endif
         // token tiles actually present (a chunk has <= 64 slots; absent tiles are not computed)
         const int nt = (it.ntok + 15) >> 4;
-#ifdef TILED_ONLY
-        tiled_body<TILED_ONLY, MODE, 4>(a, it, lds, rb0, rb1, u);
-#else
         if (nt > 3) {
             if (bits == 2) tiled_body<2, MODE, 4>(a, it, lds, rb0, rb1, u);
             else if (bits == 3) tiled_body<3, MODE, 4>(a, it, lds, rb0, rb1, u);
@@ -445,7 +442,6 @@ __global__ void __launch_bounds__(nthreads_for(MODE == GEMM_DOWN ? 512 : 2048)) 
             else if (bits == 4) tiled_body<4, MODE, 1>(a, it, lds, rb0, rb1, u);
             else tiled_body<8, MODE, 1>(a, it, lds, rb0, rb1, u);
         }
-#endif
         __syncthreads();   // the next chunk re-stages the activations
         TRACE_AT(u, 2);
         ++u;

@@ -44,6 +44,9 @@ def random_matrix(rng: np.random.Generator, R: int, K: int, bits: int, *, scale=
     return m.reshape(-1)
 
 
+W8_SCALE = (0.005 / 16, 0.02 / 16)   # W8 codes span 16x the 4-bit range: keep the output scale comparable
+
+
 def draw_bits(rng: np.random.Generator, E: int, mix) -> np.ndarray:
     if mix == "mixed":
         p = np.asarray(MIXED_P, np.float64)
@@ -52,11 +55,14 @@ def draw_bits(rng: np.random.Generator, E: int, mix) -> np.ndarray:
 
 
 def make_layer(seed: int, *, E: int = 256, H: int = 2048, I: int = 512, mix="mixed", shared: bool = False,
-               router: bool = True, zero_bias: bool = False, experts=None) -> dict:
+               router: bool = True, zero_bias: bool = False, experts=None, w8_symmetric: bool = True) -> dict:
     """A layer as the reference stores it: blob + gu_off/d_off/bits ([E + shared]) + router Wr [H, E] + bias.
 
     experts: optional iterable of expert indices to materialise (others alias expert 0's matrices); tests use it
-    to keep CPU-side work small while keeping E = 256 routing."""
+    to keep CPU-side work small while keeping E = 256 routing.
+    w8_symmetric: routed 8-bit experts in the W8A8 convention of the shared expert (per-row fp16 scales at 1/16 of
+    the 4-bit range, zero 128); False draws them like the narrower widths (random zeros: exercises the zero term,
+    but the products grow 16x and may overflow fp16 Z on large activations)."""
     rng = np.random.default_rng(seed)
     bits = draw_bits(rng, E, mix)
     Wr = (rng.standard_normal((H, E), dtype=np.float32) * np.float32(0.02)) if router else None
@@ -77,16 +83,19 @@ def make_layer(seed: int, *, E: int = 256, H: int = 2048, I: int = 512, mix="mix
             else:
                 gu_off[e], d_off[e] = first[b]
                 continue
-        g = random_matrix(rng, 2 * I, H, b)
-        d = random_matrix(rng, H, I, b)
+        if b == 8 and w8_symmetric:
+            g = random_matrix(rng, 2 * I, H, 8, scale=W8_SCALE, per_row_scale=True, symmetric=True)
+            d = random_matrix(rng, H, I, 8, scale=W8_SCALE, per_row_scale=True, symmetric=True)
+        else:
+            g = random_matrix(rng, 2 * I, H, b)
+            d = random_matrix(rng, H, I, b)
         gu_off[e] = off; chunks.append(g); off += g.size
         d_off[e] = off; chunks.append(d); off += d.size
         first.setdefault(b, (gu_off[e], d_off[e]))
     if shared:
         bits_all[E] = 8
-        sc = (0.005 / 16, 0.02 / 16)   # W8 codes span 16x the 4-bit range: keep the output scale comparable
-        g = random_matrix(rng, 2 * I, H, 8, scale=sc, per_row_scale=True, symmetric=True)
-        d = random_matrix(rng, H, I, 8, scale=sc, per_row_scale=True, symmetric=True)
+        g = random_matrix(rng, 2 * I, H, 8, scale=W8_SCALE, per_row_scale=True, symmetric=True)
+        d = random_matrix(rng, H, I, 8, scale=W8_SCALE, per_row_scale=True, symmetric=True)
         gu_off[E] = off; chunks.append(g); off += g.size
         d_off[E] = off; chunks.append(d); off += d.size
     return {"blob": np.concatenate(chunks), "gu_off": gu_off, "d_off": d_off, "bits": bits_all, "Wr": Wr,

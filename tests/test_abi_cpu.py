@@ -98,7 +98,7 @@ def test_load_rejects_bad_index(lib, tmp_path):
     assert rc == llmoe.LLMOE_EINVAL and "pruned" in err
     (tmp_path / "engine.idx").write_text(idx + "X what\n")
     rc, err = _load(tmp_path, layer=2)
-    assert rc == llmoe.LLMOE_EINVAL and "unknown line" in err
+    assert rc == llmoe.LLMOE_EINVAL and "unknown record" in err
     (tmp_path / "engine.idx").write_text(idx.replace(f"F experts_L2.bin ", "F experts_L2.bin 1", 1))
     rc, err = _load(tmp_path, layer=2)
     assert rc == llmoe.LLMOE_EINVAL and "engine.idx says" in err

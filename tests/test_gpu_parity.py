@@ -51,7 +51,7 @@ _LAYERS = {}
 def layer_for(mix, shared, seed=11):
     key = (mix, shared, seed)
     if key not in _LAYERS:
-        _LAYERS[key] = synth.make_layer(seed, mix=mix, shared=shared)
+        _LAYERS[key] = synth.make_layer(seed, mix=mix, shared=shared, w8_symmetric=False)
     return _LAYERS[key]
 
 
@@ -83,7 +83,7 @@ def test_quant_a8_bit_exact(gpu, rows):
 def test_group_products_bit_exact(gpu, bits, which):
     """Exact int32 P_g = sum code*xq - zero*Sxq for every (token, row, group), through relayout + MFMA."""
     say(f"[group_products] bits={bits} which={which}")
-    L = synth.make_layer(31 + bits, mix=bits, experts=[5])
+    L = synth.make_layer(31 + bits, mix=bits, experts=[5], w8_symmetric=False)
     G = make_gpu_layer(L, 256)
     e = 5
     R, Kw = (1024, 2048) if which == 0 else (2048, 512)
@@ -233,7 +233,7 @@ def test_full_size_batch_invariance(gpu, T, mix, shared, pool, kind):
     that size; a token's output depends only on its own routing block, so the rows of a few whole 32-token
     blocks must equal, bit for bit, the oracle run on those blocks alone (indices, weights and outputs)."""
     say(f"[full size] T={T} mix={mix} shared={shared} pool={pool} {kind}")
-    L = synth.make_layer(7 + T, mix=mix, shared=shared, zero_bias=kind is not None)
+    L = synth.make_layer(7 + T, mix=mix, shared=shared, zero_bias=kind is not None, w8_symmetric=False)
     x = synth.make_x(900 + T, T, outlier_frac=0.01 if mix == "mixed" else 0.0)
     lg = None
     if kind == "zipf":
