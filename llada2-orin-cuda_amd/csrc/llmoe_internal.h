@@ -169,6 +169,15 @@ __device__ __forceinline__ uint64_t wave_incl_scan(uint64_t v) {
     return (uint64_t(wave_incl_scan(uint32_t(v >> 32))) << 32) | wave_incl_scan(uint32_t(v));
 }
 
+// The gate_up output fp16(SiLU(g) u) with the hardware transcendentals (v_exp_f32, v_rcp_f32) and conversion
+// (v_cvt_f16_f32): the precision of the reference's own __expf / __fdividef / __float2half (engine/moe_i8.cu:221),
+// within the fp32-stage tolerance, not bit-identical to silu_f32 / f32_to_f16_bits.
+__device__ __forceinline__ uint16_t silu_mul_f16_fast(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+    const float y = (g * __builtin_amdgcn_rcpf(1.0f + e)) * u;
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(y));
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
 }
@@ -193,6 +202,9 @@ struct GemmArgs {
     int32_t* P;                 // group-products out [n, R, K/128] (test entry)
     const int* tstart;          // tiled: [G + 1] first task of each workgroup (the work partition above)
     int accumulate;             // GEMM_DENSE: Y += acc instead of Y = acc
+    int fast;                   // gate_up: SiLU by the hardware exp / reciprocal and fp16 conversion
+    float* out_acc;             // down, when set: out_acc[out_row[slot]] += w_slot * acc (atomic; Y not written)
+    const int* out_row;         // down: the token of each slot
 };
 
 // GEMM_DENSE: a plain W.A8 projection [R, 2048] (rows in packlib order), out Y[token, r] = acc (or += acc)
@@ -215,7 +227,9 @@ int tiled_grid(int mode);
 hipError_t launch_tiled_gemm(int mode, const GemmArgs& a, hipStream_t st);
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, int R, int K, int bits, int gate_up, hipStream_t st);
 hipError_t launch_quant_a8(const float* x, int rows, int cols, int8_t* q, float* s, int* sum, hipStream_t st);
-hipError_t launch_fwht_a8(const uint16_t* Z, int nslots, int8_t* q, float* s, int* sum, hipStream_t st);
+// zero != nullptr: the kernel also clears zero[0 .. nzero) (the fused combine's target, ahead of the down GEMM)
+hipError_t launch_fwht_a8(const uint16_t* Z, int nslots, int8_t* q, float* s, int* sum, float* zero, size_t nzero,
+                          hipStream_t st);
 // combine + FWHT-2048 un-rotation + residual into h + next-layer RMSNorm / rotation / A8 (H = 2048)
 hipError_t launch_combine_norm(const float* Y, const int* tok_slots, int T, int kk, int K1, const float* signs,
                                float eps, float* h, int8_t* q, float* s, int* sum, hipStream_t st);

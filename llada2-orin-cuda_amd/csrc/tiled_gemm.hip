@@ -10,8 +10,9 @@
 // into MFMA A operands and used for all 4 token tiles, and the fp32 accumulators of the (strip, token tile) pairs
 // stay in registers until the fused epilogue. No barrier inside a row block, so the waves (2 per SIMD; 4 for
 // down) drift freely and one wave's MFMAs overlap another's vector epilogue.
-// Zero points: for 2/3-bit codes the zero is subtracted while unpacking (a v_perm_b32 lookup of c - z); 4-bit
-// codes and 8-bit codes (stored c - 128) put the zero term zero * (-Sxq) of the lane's four output rows on the
+// Zero points: for 2/3-bit codes the zero is subtracted while unpacking (a v_perm_b32 lookup of c - z), for 4-bit
+// codes bytewise (c + 128 - z, then ^ 0x80) when the tile serves two or more token tiles; 8-bit codes (stored
+// c - 128) and 4-bit codes of one-tile chunks put the zero term zero * (-Sxq) of the lane's four output rows on the
 // MFMA's initial accumulator instead. Either way the accumulator starts from I2F_BIAS, so its bits end as the
 // float 1.5 * 2^23 + P_g and one subtraction gives float(P_g).
 #include <type_traits>
@@ -69,11 +70,13 @@ template <int BITS>
 __device__ __forceinline__ void load_s0(const uint8_t* p, int lane, Codes<BITS>& r) {
     r.s0 = *reinterpret_cast<const u4*>(p + BITS * 1024 + 32 * (lane >> 4));
 }
-template <int BITS>
+// ZACC: the zero term rides on the MFMA accumulator (zeros of the lane's four output rows); otherwise the zero is
+// subtracted while unpacking (zeros of the lane's A-operand row)
+template <int BITS, bool ZACC>
 __device__ __forceinline__ void load_late(const uint8_t* p, int lane, Late& r) {
     const uint8_t* m = p + BITS * 1024;
     r.s1 = *reinterpret_cast<const u4*>(m + 32 * (lane >> 4) + 16);
-    r.z = *reinterpret_cast<const u4*>(m + 128 + 16 * (BITS >= 4 ? (lane >> 4) : ((lane & 15) >> 2)));
+    r.z = *reinterpret_cast<const u4*>(m + 128 + 16 * (ZACC ? (lane >> 4) : ((lane & 15) >> 2)));
     if constexpr (BITS == 3) r.hi = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p + 2 * 1024) + lane);
 }
 
@@ -82,7 +85,7 @@ __device__ __forceinline__ void load_late(const uint8_t* p, int lane, Late& r) {
 // the byte sequence -3 .. 3 (one v_alignbyte_b32); the 3-bit table is built as (c | 0x80) - z per byte, which
 // never borrows across bytes (c + 128 - z > 0), with ^ 0x80 turning the biased byte into the two's complement
 // of c - z. 4/8-bit: the codes as they are (the zero term is on the accumulator).
-template <int BITS>
+template <int BITS, bool ZACC>
 __device__ __forceinline__ void unpack_a(const Codes<BITS>& r, const Late& lt, int tau, int lane, uint32_t (&D)[8]) {
     if constexpr (BITS == 8) {
         const u4& a = r.c[2 * tau];
@@ -122,12 +125,22 @@ __device__ __forceinline__ void unpack_a(const Codes<BITS>& r, const Late& lt, i
                 for (int s = 0; s < 8; ++s) D[s] = __builtin_amdgcn_perm(t_hi, t_lo, D[s]);
             }
             return;
-        } else {
+        } else if constexpr (ZACC) {
             const u4& u = r.c[tau];
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 D[2 * m] = u[m] & 0x0F0F0F0Fu;
                 D[2 * m + 1] = (u[m] >> 4) & 0x0F0F0F0Fu;
+            }
+        } else {
+            // c + 128 - z per byte never borrows across bytes (c, z in 0 .. 15); ^ 0x80 gives the int8 c - z
+            const u4& u = r.c[tau];
+            const uint32_t z = (lt.z[tau] >> (8 * (lane & 3))) & 0xFFu;
+            const uint32_t k = 0x80808080u - z * 0x01010101u;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                D[2 * m] = ((u[m] & 0x0F0F0F0Fu) + k) ^ 0x80808080u;
+                D[2 * m + 1] = (((u[m] >> 4) & 0x0F0F0F0Fu) + k) ^ 0x80808080u;
             }
         }
     }
@@ -222,6 +235,9 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
     constexpr int NSB = DOWN ? 1 : 4, K = NSB * SB_K, G = K / GROUP;
     constexpr int S = tiled_spw(DOWN, BITS), NW = nw_for(K);
     constexpr size_t SBB = sb_bytes(BITS);
+    // 4-bit codes subtract the zero while unpacking once the unpacked tile serves two or more token tiles (16 VALU
+    // per tile against 8 per token tile for the accumulator's zero term)
+    constexpr bool ZACC = BITS == 8 || (BITS == 4 && NTILE == 1);
     const int lane = threadIdx.x & 63, q = lane >> 4, col = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int strip0 = (rb * NW + wave) * S;
@@ -236,8 +252,8 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
 #pragma unroll
         for (int i = 0; i < Codes<BITS>::N; ++i) load_code<BITS>(sbp(s, 0), lane, i, cd[s]);
         load_s0<BITS>(sbp(s, 0), lane, cd[s]);
-        load_late<BITS>(sbp(s, 0), lane, lt[0][s]);
-        if constexpr (NSB > 1) load_late<BITS>(sbp(s, 1), lane, lt[1][s]);
+        load_late<BITS, ZACC>(sbp(s, 0), lane, lt[0][s]);
+        if constexpr (NSB > 1) load_late<BITS, ZACC>(sbp(s, 1), lane, lt[1][s]);
     }
     float acc[S][NTILE][4];
 #pragma unroll
@@ -257,20 +273,20 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
         for (int s = 0; s < S; ++s) {
             const Late& l = lt[sb % 2][s];
             uint32_t Dw[8];
-            unpack_a<BITS>(cd[s], l, tau, lane, Dw);
+            unpack_a<BITS, ZACC>(cd[s], l, tau, lane, Dw);
             A0[s] = v4i{int(Dw[0]), int(Dw[1]), int(Dw[2]), int(Dw[3])};
             A1[s] = v4i{int(Dw[4]), int(Dw[5]), int(Dw[6]), int(Dw[7])};
             const u4& sv = tau < 2 ? cd[s].s0 : l.s1;
             swp[s][0] = sv[(tau & 1) * 2];
             swp[s][1] = sv[(tau & 1) * 2 + 1];
-            if constexpr (BITS >= 4) {
+            if constexpr (ZACC) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) zz[s][v] = int((l.z[tau] >> (8 * v)) & 0xFFu) - (BITS == 8 ? 128 : 0);
             }
             // registers tile tau alone used: refill with the next superblock; after the last tile the
             // superblock-wide registers take the superblock after next
             if constexpr (sb + 1 < NSB) refill_after<BITS, tau>(sbp(s, sb + 1), lane, cd[s]);
-            if constexpr (tau == 3 && sb + 2 < NSB) load_late<BITS>(sbp(s, sb + 2), lane, lt[sb % 2][s]);
+            if constexpr (tau == 3 && sb + 2 < NSB) load_late<BITS, ZACC>(sbp(s, sb + 2), lane, lt[sb % 2][s]);
         }
         // software pipeline over the token tiles: the MFMAs of tile nt are issued before the fp32 epilogue of
         // tile nt-1, and the B operands are read one tile ahead
@@ -291,7 +307,7 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
         v4i Bn0 = *bptr(0, 0), Bn1 = *bptr(0, 1);
         float xsnext = ss[g * TILED_NTOK + col];
         int nsnext = 0;
-        if constexpr (BITS >= 4) nsnext = sq[g * TILED_NTOK + col];
+        if constexpr (ZACC) nsnext = sq[g * TILED_NTOK + col];
         static_for<0, NTILE + 1>([&](auto tc) {
             constexpr int nt = decltype(tc)::value;
             v4i Cc[S];
@@ -304,11 +320,11 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
                     Bn0 = *bptr(nt + 1, 0);
                     Bn1 = *bptr(nt + 1, 1);
                     xsnext = ss[g * TILED_NTOK + (nt + 1) * 16 + col];
-                    if constexpr (BITS >= 4) nsnext = sq[g * TILED_NTOK + (nt + 1) * 16 + col];
+                    if constexpr (ZACC) nsnext = sq[g * TILED_NTOK + (nt + 1) * 16 + col];
                 }
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
-                    if constexpr (BITS >= 4)
+                    if constexpr (ZACC)
                         Cc[s] = v4i{__mul24(zz[s][0], nsum) + I2F_BIAS, __mul24(zz[s][1], nsum) + I2F_BIAS,
                                     __mul24(zz[s][2], nsum) + I2F_BIAS, __mul24(zz[s][3], nsum) + I2F_BIAS};
                     else
@@ -360,9 +376,20 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
                     }
                     *yp = y;
                 } else if constexpr (MODE == GEMM_GATE_UP) {
-                    const uint32_t z0 = f32_to_f16_bits(silu_f32(acc[s][nt][0]) * acc[s][nt][1]);
-                    const uint32_t z1 = f32_to_f16_bits(silu_f32(acc[s][nt][2]) * acc[s][nt][3]);
+                    uint32_t z0, z1;
+                    if (a.fast) {
+                        z0 = silu_mul_f16_fast(acc[s][nt][0], acc[s][nt][1]);
+                        z1 = silu_mul_f16_fast(acc[s][nt][2], acc[s][nt][3]);
+                    } else {
+                        z0 = f32_to_f16_bits(silu_f32(acc[s][nt][0]) * acc[s][nt][1]);
+                        z1 = f32_to_f16_bits(silu_f32(acc[s][nt][2]) * acc[s][nt][3]);
+                    }
                     *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
+                } else if (a.out_acc) {   // fused combine: the token's output row accumulates w acc
+                    const float w = a.slot_weight[slot];
+                    float* o = a.out_acc + size_t(a.out_row[slot]) * a.R + 16 * strip + 4 * q;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) unsafeAtomicAdd(o + v, w * acc[s][nt][v]);
                 } else {
                     const float w = a.slot_weight[slot];
                     *reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q) =

@@ -21,6 +21,7 @@ LIB_PATH = _HERE / "libllmoe.so"
 
 LLMOE_OK = 0
 SCRATCH_MAX_TOKENS = 64   # LLMOE_SCRATCH_MAX_TOKENS of include/llmoe.h
+NUMERICS_EXACT, NUMERICS_FAST = 0, 1
 LLMOE_EINVAL = -1   # bad argument or shape
 LLMOE_ENOMEM = -2
 LLMOE_EHIP = -3
@@ -65,7 +66,7 @@ EXPORTS = [
     "llmoe_experts", "llmoe_experts_norm", "llmoe_layer_forward", "llmoe_layer_buffers", "llmoe_layer_weight_bytes",
     "llmoe_group_products", "llmoe_layer_set_profiling", "llmoe_layer_stage_ms", "llmoe_layer_time_stage", "llmoe_layers_time_stage",
     "llmoe_layer_load", "llmoe_model_signs", "llmoe_dense_create", "llmoe_dense_destroy", "llmoe_dense_forward",
-    "llmoe_last_error", "llmoe_experts_scratch",
+    "llmoe_last_error", "llmoe_experts_scratch", "llmoe_layer_set_numerics",
 ]
 
 STAGES = ["quant", "router", "route", "dispatch", "gate_up", "fwht", "down", "combine"]
@@ -103,6 +104,7 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.llmoe_layer_weight_bytes.argtypes = [vp, ctypes.POINTER(sz)]
     lib.llmoe_group_products.argtypes = [vp, i, i, vp, vp, i, vp, vp]
     lib.llmoe_layer_set_profiling.argtypes = [vp, i]
+    lib.llmoe_layer_set_numerics.argtypes = [vp, i]
     lib.llmoe_layer_stage_ms.argtypes = [vp, ctypes.POINTER(ctypes.c_float)]
     lib.llmoe_layer_time_stage.argtypes = [vp, i, i, vp, ctypes.POINTER(ctypes.c_float)]
     lib.llmoe_layers_time_stage.argtypes = [ctypes.POINTER(ctypes.c_void_p), i, i, i, vp, ctypes.POINTER(ctypes.c_float)]
@@ -239,6 +241,10 @@ class Layer:
         _check(self.lib.llmoe_group_products(self.handle, expert, which, _ptr(xq), _ptr(xsum), n, _ptr(P),
                                              _stream(stream)))
         return P
+
+    def set_numerics(self, fast: bool) -> None:
+        """LLMOE_NUMERICS_FAST (hardware SiLU, combine fused into the down GEMM) or LLMOE_NUMERICS_EXACT."""
+        _check(self.lib.llmoe_layer_set_numerics(self.handle, NUMERICS_FAST if fast else NUMERICS_EXACT))
 
     def set_profiling(self, on: bool) -> None:
         _check(self.lib.llmoe_layer_set_profiling(self.handle, int(on)))

@@ -430,10 +430,11 @@ static void free_unpacked(unpacked* u) {
     free(u->gu_c); free(u->gu_z); free(u->gu_s); free(u->d_c); free(u->d_z); free(u->d_s);
 }
 
-int orc_experts(const orc_layer* L, const int8_t* xq, const float* xs, const int32_t* xsum, int T,
-                const int32_t* count, const int32_t* start, const int32_t* slot_token, const float* slot_weight,
-                const int32_t* tok_slots, uint16_t* Z, int8_t* zq, float* zs, int32_t* zsum, float* Y, float* out,
-                int nthreads) {
+/* zin != NULL: the gate_up outputs Z of every slot are given (gate_up is skipped; xq, xs, xsum unused) */
+static int experts_impl(const orc_layer* L, const int8_t* xq, const float* xs, const int32_t* xsum,
+                        const uint16_t* zin, int T, const int32_t* count, const int32_t* start,
+                        const int32_t* slot_token, const float* slot_weight, const int32_t* tok_slots, uint16_t* Z,
+                        int8_t* zq, float* zs, int32_t* zsum, float* Y, float* out, int nthreads) {
     const int H = L->H, I = L->I, E = L->E, K = L->K, GH = H / GROUP, GI = I / GROUP;
     const int nexp = E + (L->has_shared ? 1 : 0);
     const int S = T * K + (L->has_shared ? T : 0);
@@ -467,11 +468,16 @@ int orc_experts(const orc_layer* L, const int8_t* xq, const float* xs, const int
             unpack_expert(L, e, &u);
             for (int i = 0; i < n; ++i) {
                 const int slot = s0 + i, tok = slot_token[slot];
-                /* gate_up: packed rows -> logical rows (gate 0..I-1, up I..2I-1) */
-                orc_group_products(u.gu_c, u.gu_z, 2 * I, H, xq + (size_t)tok * H, xsum + (size_t)tok * GH, P);
-                for (int p = 0; p < 2 * I; ++p)
-                    gacc[perm[p]] = row_epilogue(P + (size_t)p * GH, u.gu_s + (size_t)p * GH, xs + (size_t)tok * GH, GH);
-                for (int j = 0; j < I; ++j) zrow[j] = orc_f32_to_f16(orc_silu(gacc[j]) * gacc[I + j]);
+                if (zin) {
+                    memcpy(zrow, zin + (size_t)slot * I, sizeof(zrow));
+                } else {
+                    /* gate_up: packed rows -> logical rows (gate 0..I-1, up I..2I-1) */
+                    orc_group_products(u.gu_c, u.gu_z, 2 * I, H, xq + (size_t)tok * H, xsum + (size_t)tok * GH, P);
+                    for (int p = 0; p < 2 * I; ++p)
+                        gacc[perm[p]] = row_epilogue(P + (size_t)p * GH, u.gu_s + (size_t)p * GH, xs + (size_t)tok * GH,
+                                                     GH);
+                    for (int j = 0; j < I; ++j) zrow[j] = orc_f32_to_f16(orc_silu(gacc[j]) * gacc[I + j]);
+                }
                 fwht_a8_one(zrow, qrow, srow, sumrow);
                 if (Z) memcpy(Z + (size_t)slot * I, zrow, sizeof(zrow));
                 if (zq) memcpy(zq + (size_t)slot * I, qrow, sizeof(qrow));
@@ -499,6 +505,21 @@ int orc_experts(const orc_layer* L, const int8_t* xq, const float* xs, const int
     }
     if (!Y) free(Yw);
     return err ? -1 : 0;
+}
+
+int orc_experts(const orc_layer* L, const int8_t* xq, const float* xs, const int32_t* xsum, int T,
+                const int32_t* count, const int32_t* start, const int32_t* slot_token, const float* slot_weight,
+                const int32_t* tok_slots, uint16_t* Z, int8_t* zq, float* zs, int32_t* zsum, float* Y, float* out,
+                int nthreads) {
+    return experts_impl(L, xq, xs, xsum, NULL, T, count, start, slot_token, slot_weight, tok_slots, Z, zq, zs, zsum, Y,
+                        out, nthreads);
+}
+
+int orc_experts_from_z(const orc_layer* L, const uint16_t* Z, int T, const int32_t* count, const int32_t* start,
+                       const int32_t* slot_token, const float* slot_weight, const int32_t* tok_slots, int8_t* zq,
+                       float* zs, int32_t* zsum, float* Y, float* out, int nthreads) {
+    return experts_impl(L, NULL, NULL, NULL, Z, T, count, start, slot_token, slot_weight, tok_slots, NULL, zq, zs,
+                        zsum, Y, out, nthreads);
 }
 
 /* ------------------------------------------------------------------------------------------------------------

@@ -49,6 +49,8 @@ def lib() -> ctypes.CDLL:
         L.orc_experts.argtypes = [ctypes.POINTER(OrcLayer), vp, vp, vp, i, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
                                   vp, i]
         L.orc_experts.restype = i
+        L.orc_experts_from_z.argtypes = [ctypes.POINTER(OrcLayer), vp, i, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i]
+        L.orc_experts_from_z.restype = i
         L.orc_reference_f64.argtypes = [ctypes.POINTER(OrcLayer), vp, i, vp, vp, vp, i]
         L.orc_reference_f64.restype = i
         L.orc_combine_norm.argtypes = [vp, vp, i, i, i, vp, f, vp, vp, vp, vp]
@@ -231,6 +233,26 @@ class Layer:
         if rc != 0:
             raise RuntimeError(f"orc_experts failed: {rc}")
         return dict(out=out, Y=Y, Z=Z, zq=zq, zs=zs, zsum=zsum, **dsp)
+
+    def experts_from_z(self, Z, topk, topw, nthreads=0):
+        """The expert stage after gate_up, from given fp16 Z [S, I] bits: FWHT-512 + A8, down, combine."""
+        L = self.layer
+        H, I, E = L["H"], L["I"], L["E"]
+        T = topk.shape[0]
+        dsp = dispatch(topk, topw, E, L["shared"])
+        S = dsp["slot_token"].size
+        Z = np.ascontiguousarray(Z, np.uint16).reshape(S, I)
+        zq = np.zeros((S, I), np.int8)
+        zs = np.zeros((S, 4), np.float32)
+        zsum = np.zeros((S, 4), np.int32)
+        Y = np.zeros((S, H), np.float32)
+        out = np.zeros((T, H), np.float32)
+        rc = lib().orc_experts_from_z(ctypes.byref(self.c), _p(Z), T, _p(dsp["count"]), _p(dsp["start"]),
+                                      _p(dsp["slot_token"]), _p(dsp["slot_weight"]), _p(dsp["tok_slots"]), _p(zq),
+                                      _p(zs), _p(zsum), _p(Y), _p(out), nthreads)
+        if rc != 0:
+            raise RuntimeError(f"orc_experts_from_z failed: {rc}")
+        return dict(out=out, Y=Y, zq=zq, zs=zs, zsum=zsum, **dsp)
 
     def reference_f64(self, x, topk, topw, nthreads=0):
         T = x.shape[0]

@@ -350,3 +350,13 @@ def test_dense_against_reference(bits):
     # accumulate: y0 + epilogue, one fp32 add per element
     y0 = gen.normal(3100, y.shape).astype(np.float32)
     np.testing.assert_array_equal(O.dense(blob, R, K, bits, xq, xs, xsum, y=y0), y0 + y)
+
+
+def test_experts_from_z_reproduces_the_expert_stage():
+    """orc_experts_from_z on the Z of orc_experts gives the same A8, slot outputs and combine, bit for bit."""
+    layer = synth.make_layer(8, E=64, mix="mixed", shared=True)
+    x = synth.make_x(3, 8)
+    r = O.Layer(layer).forward(x, C=64)
+    rz = O.Layer(layer).experts_from_z(r["Z"], r["topk"], r["topw"])
+    for k in ("zq", "zs", "zsum", "Y", "out"):
+        np.testing.assert_array_equal(np.asarray(rz[k]).view(np.uint8), np.asarray(r[k]).view(np.uint8), err_msg=k)
