@@ -125,15 +125,13 @@ int llmoe_layer_forward(llmoe_layer* layer, const float* x, const float* logits,
 
 /* Numerics of a layer's expert stage (default LLMOE_NUMERICS_EXACT).
  *   EXACT: every stage follows one fixed fp32 operation sequence (SiLU with a polynomial exp and a correctly rounded
- *          divide, integer round-to-nearest-even to fp16, the combine summed in rank order from the slot outputs
- *          Y), so results are bit-identical run to run and to the CPU restatement of the reference.
+ *          divide, integer round-to-nearest-even to fp16), so results are bit-identical run to run and to the CPU
+ *          restatement of the reference.
  *   FAST:  the SiLU of gate_up uses the hardware exp, reciprocal and fp16 conversion -- the precision of the
- *          reference's own __expf / __fdividef / __float2half (engine/moe_i8.cu:221) -- and the combine is fused
- *          into the down GEMM, which adds w * acc of every slot into its token's output row with atomic adds (no
- *          Y round trip through HBM, no combine launch; Y in llmoe_layer_buffers is then not written). The int32
- *          expert products are unchanged (exact); fp32 stages agree with EXACT within the contract's 1e-3
- *          relative tolerance, and the summation order of the 9 slot outputs of a token varies run to run.
- * A configuration call (it allocates the fused norm epilogue's buffer on first use): not for graph capture. */
+ *          reference's own __expf / __fdividef / __float2half (engine/moe_i8.cu:221). Z then differs from EXACT by
+ *          at most one fp16 rounding step; the int32 expert products and every later stage are computed exactly as
+ *          in EXACT from that Z, and the layer output agrees with EXACT within the contract's 1e-3 tolerance.
+ * Takes effect from the next llmoe_experts / llmoe_experts_norm / llmoe_layer_forward call on the layer. */
 #define LLMOE_NUMERICS_EXACT 0
 #define LLMOE_NUMERICS_FAST 1
 int llmoe_layer_set_numerics(llmoe_layer* layer, int mode);
@@ -188,8 +186,7 @@ int llmoe_layer_stage_ms(llmoe_layer* layer, float* ms);
 /* Re-launch one expert stage of the latest llmoe_experts / llmoe_experts_norm call (LLMOE_STAGE_GATE_UP, _FWHT,
  * _DOWN or _COMBINE) `reps` times back to back between two HIP events on `stream`, and return the average
  * milliseconds per launch (the kernel's steady-state duration). The stages are idempotent except the combine of
- * an llmoe_experts_norm call, which adds into h again on every repeat, and (LLMOE_NUMERICS_FAST) the down GEMM,
- * which adds into the output again. Waits for completion. */
+ * an llmoe_experts_norm call, which adds into h again on every repeat. Waits for completion. */
 int llmoe_layer_time_stage(llmoe_layer* layer, int stage, int reps, llmoe_stream stream, float* avg_ms);
 
 /* As llmoe_layer_time_stage over n layers launched in turn (layer 0, 1, .., n-1, repeated `reps` times): with

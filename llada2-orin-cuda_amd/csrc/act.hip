@@ -59,12 +59,9 @@ __global__ void __launch_bounds__(256) quant_a8_kernel(const float* __restrict__
 // ascending h. The group quantiser multiplies by 1/s. Logical order out. grid ceil(n/4), 256 threads.
 __global__ void __launch_bounds__(256) fwht_a8_kernel(const uint16_t* __restrict__ Z, int nslots,
                                                       int8_t* __restrict__ q, float* __restrict__ s,
-                                                      int* __restrict__ sum, float* __restrict__ zero, size_t nzero4) {
+                                                      int* __restrict__ sum) {
     const int lane = threadIdx.x & 63;
     const int slot = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (zero)   // the fused combine's target: cleared here, read-modify-written only by the down GEMM that follows
-        for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < nzero4; i += size_t(gridDim.x) * 256)
-            reinterpret_cast<float4*>(zero)[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (slot >= nslots) return;
     const uint4 raw = *reinterpret_cast<const uint4*>(Z + size_t(slot) * 512 + 8 * lane);
     const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
@@ -292,11 +289,9 @@ hipError_t launch_quant_a8(const float* x, int rows, int cols, int8_t* q, float*
     return hipGetLastError();
 }
 
-hipError_t launch_fwht_a8(const uint16_t* Z, int nslots, int8_t* q, float* s, int* sum, float* zero, size_t nzero,
-                          hipStream_t st) {
+hipError_t launch_fwht_a8(const uint16_t* Z, int nslots, int8_t* q, float* s, int* sum, hipStream_t st) {
     if (nslots <= 0) return hipSuccess;
-    if (nzero % 4) return hipErrorInvalidValue;
-    fwht_a8_kernel<<<(nslots + 3) / 4, 256, 0, st>>>(Z, nslots, q, s, sum, zero, nzero / 4);
+    fwht_a8_kernel<<<(nslots + 3) / 4, 256, 0, st>>>(Z, nslots, q, s, sum);
     return hipGetLastError();
 }
 

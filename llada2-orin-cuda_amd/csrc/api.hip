@@ -109,10 +109,7 @@ struct llmoe_layer {
     size_t chunks_cap = 0;                          // tiled chunks
     int g_gu = 0, g_dn = 0;                         // tiled GEMM grids (workgroups of the work partition)
     int* tstart = nullptr;                          // [g_gu + 1 + g_dn + 1] tiled work partition
-    // numerics: fast = hardware SiLU transcendentals and the combine fused into the down GEMM (atomic adds)
-    bool fast = false;
-    float* ysum = nullptr;                          // fast llmoe_experts_norm: the combined rows [max_tokens, H]
-    int32_t* ident = nullptr;                       // [max_tokens] t -> t (one "slot" per token for combine_norm)
+    bool fast = false;                              // numerics: the gate_up SiLU by the hardware transcendentals
     // routing state
     int routed_T = -1, ntok = 16, max_items = 0;
     bool tiled = false;                             // the routing of routed_T may have tiled units
@@ -125,7 +122,6 @@ struct llmoe_layer {
     float* last_out = nullptr;
     NormOut last_norm{};
     Inter last_w{};
-    float* last_zero = nullptr;                     // fast mode: the fused combine's target, cleared by the FWHT kernel
     int last_S = 0, last_T = 0, last_nt = 1;
     bool last_tiled = false;
     bool have_last = false;
@@ -449,9 +445,6 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     g.xq = xq; g.xs = xs; g.xsum = xsum;
     g.K = H; g.R = 2 * I; g.Z = w.Z;
     g.fast = L->fast ? 1 : 0;
-    // fast mode: the down GEMM accumulates w acc straight into the output rows (or, ahead of the norm epilogue,
-    // into the combined-row buffer), which the FWHT kernel clears first
-    float* target = !L->fast ? nullptr : no.h ? L->ysum : out;
     GemmArgs tg = g;
     tg.items = L->tunits_gu;
     tg.tstart = L->tstart;
@@ -462,7 +455,7 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     HIPCHECK(launch_gemm(GEMM_GATE_UP, g, tg, L->tiled, st));
     L->mark(LLMOE_STAGE_GATE_UP, true, st);
     L->mark(LLMOE_STAGE_FWHT, false, st);
-    HIPCHECK(launch_fwht_a8(w.Z, S, w.zq, w.zs, w.zsum, target, target ? size_t(T) * H : 0, st));
+    HIPCHECK(launch_fwht_a8(w.Z, S, w.zq, w.zs, w.zsum, st));
     L->mark(LLMOE_STAGE_FWHT, true, st);
     // down: B rows are slot rows of Z'
     g.items = L->units_dn;
@@ -472,8 +465,6 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     g.xq = w.zq; g.xs = w.zs; g.xsum = w.zsum;
     g.K = I; g.R = H; g.Z = nullptr; g.Y = w.Y;
     g.fast = 0;
-    g.out_acc = target;
-    g.out_row = L->slot_token;
     tg = g;
     tg.items = L->tunits_dn;
     tg.tstart = L->tstart + L->g_gu + 1;
@@ -481,16 +472,12 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     L->last_dn = g;
     L->last_tdn = tg;
     L->last_S = S; L->last_T = T; L->last_tiled = L->tiled; L->last_out = out; L->last_norm = no; L->last_w = w;
-    L->last_zero = target;
     L->have_last = true;
     L->mark(LLMOE_STAGE_DOWN, false, st);
     HIPCHECK(launch_gemm(GEMM_DOWN, g, tg, L->tiled, st));
     L->mark(LLMOE_STAGE_DOWN, true, st);
     L->mark(LLMOE_STAGE_COMBINE, false, st);
-    if (target) {
-        if (no.h)
-            HIPCHECK(launch_combine_norm(L->ysum, L->ident, T, 1, 1, no.signs, no.eps, no.h, no.q, no.s, no.sum, st));
-    } else if (no.h)
+    if (no.h)
         HIPCHECK(launch_combine_norm(w.Y, L->tok_slots, T, K + (d.has_shared ? 1 : 0), K + 1, no.signs, no.eps, no.h,
                                      no.q, no.s, no.sum, st));
     else
@@ -596,14 +583,6 @@ int llmoe_layer_forward(llmoe_layer* L, const float* x, const float* logits, int
 int llmoe_layer_set_numerics(llmoe_layer* L, int mode) {
     if (int rc = check_layer(L)) return rc;
     if (mode != LLMOE_NUMERICS_EXACT && mode != LLMOE_NUMERICS_FAST) return fail(LLMOE_EINVAL, "numerics mode %d", mode);
-    if (mode == LLMOE_NUMERICS_FAST && !L->ysum) {   // the combined-row buffer of the fused norm epilogue
-        const size_t Tm = size_t(L->d.max_tokens);
-        if (L->alloc(&L->ysum, Tm * L->d.hidden) != hipSuccess || L->alloc(&L->ident, Tm) != hipSuccess)
-            return fail(LLMOE_ENOMEM, "hipMalloc fast-mode buffers");
-        std::vector<int32_t> id(Tm);
-        for (size_t t = 0; t < Tm; ++t) id[t] = int32_t(t);
-        HIPCHECK(hipMemcpy(L->ident, id.data(), Tm * sizeof(int32_t), hipMemcpyHostToDevice));
-    }
     L->fast = mode == LLMOE_NUMERICS_FAST;
     return LLMOE_OK;
 }
@@ -637,15 +616,8 @@ hipError_t relaunch_stage(llmoe_layer* L, int stage, hipStream_t st) {
     switch (stage) {
         case LLMOE_STAGE_GATE_UP: return launch_gemm(GEMM_GATE_UP, L->last_gu, L->last_tgu, L->last_tiled, st);
         case LLMOE_STAGE_DOWN: return launch_gemm(GEMM_DOWN, L->last_dn, L->last_tdn, L->last_tiled, st);
-        case LLMOE_STAGE_FWHT:
-            return launch_fwht_a8(L->last_w.Z, L->last_S, L->last_w.zq, L->last_w.zs, L->last_w.zsum, L->last_zero,
-                                  L->last_zero ? size_t(L->last_T) * d.hidden : 0, st);
+        case LLMOE_STAGE_FWHT: return launch_fwht_a8(L->last_w.Z, L->last_S, L->last_w.zq, L->last_w.zs, L->last_w.zsum, st);
         case LLMOE_STAGE_COMBINE:
-            if (L->last_zero) {   // fast mode: fused into the down GEMM; only the norm epilogue remains
-                if (!L->last_norm.h) return hipSuccess;
-                return launch_combine_norm(L->ysum, L->ident, L->last_T, 1, 1, L->last_norm.signs, L->last_norm.eps,
-                                           L->last_norm.h, L->last_norm.q, L->last_norm.s, L->last_norm.sum, st);
-            }
             if (L->last_norm.h)   // re-adds into h: each repeat moves the residual stream on by one more layer
                 return launch_combine_norm(L->last_w.Y, L->tok_slots, L->last_T, d.top_k + (d.has_shared ? 1 : 0),
                                            d.top_k + 1, L->last_norm.signs, L->last_norm.eps, L->last_norm.h,

@@ -363,11 +363,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
                             z1 = f32_to_f16_bits(silu_f32(acc[nt][2]) * acc[nt][3]);
                         }
                         *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
-                    } else if (a.out_acc) {   // fused combine: the token's output row accumulates w acc
-                        const float w = wts[nt];
-                        float* o = a.out_acc + size_t(a.out_row[slot]) * a.R + 16 * strip + 4 * q;
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) unsafeAtomicAdd(o + v, w * acc[nt][v]);
                     } else {
                         const float w = wts[nt];
                         *reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q) =

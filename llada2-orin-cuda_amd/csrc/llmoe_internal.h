@@ -203,8 +203,6 @@ struct GemmArgs {
     const int* tstart;          // tiled: [G + 1] first task of each workgroup (the work partition above)
     int accumulate;             // GEMM_DENSE: Y += acc instead of Y = acc
     int fast;                   // gate_up: SiLU by the hardware exp / reciprocal and fp16 conversion
-    float* out_acc;             // down, when set: out_acc[out_row[slot]] += w_slot * acc (atomic; Y not written)
-    const int* out_row;         // down: the token of each slot
 };
 
 // GEMM_DENSE: a plain W.A8 projection [R, 2048] (rows in packlib order), out Y[token, r] = acc (or += acc)
@@ -227,9 +225,7 @@ int tiled_grid(int mode);
 hipError_t launch_tiled_gemm(int mode, const GemmArgs& a, hipStream_t st);
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, int R, int K, int bits, int gate_up, hipStream_t st);
 hipError_t launch_quant_a8(const float* x, int rows, int cols, int8_t* q, float* s, int* sum, hipStream_t st);
-// zero != nullptr: the kernel also clears zero[0 .. nzero) (the fused combine's target, ahead of the down GEMM)
-hipError_t launch_fwht_a8(const uint16_t* Z, int nslots, int8_t* q, float* s, int* sum, float* zero, size_t nzero,
-                          hipStream_t st);
+hipError_t launch_fwht_a8(const uint16_t* Z, int nslots, int8_t* q, float* s, int* sum, hipStream_t st);
 // combine + FWHT-2048 un-rotation + residual into h + next-layer RMSNorm / rotation / A8 (H = 2048)
 hipError_t launch_combine_norm(const float* Y, const int* tok_slots, int T, int kk, int K1, const float* signs,
                                float eps, float* h, int8_t* q, float* s, int* sum, hipStream_t st);

@@ -243,7 +243,7 @@ class Layer:
         return P
 
     def set_numerics(self, fast: bool) -> None:
-        """LLMOE_NUMERICS_FAST (hardware SiLU, combine fused into the down GEMM) or LLMOE_NUMERICS_EXACT."""
+        """LLMOE_NUMERICS_FAST (the gate_up SiLU by the hardware transcendentals) or LLMOE_NUMERICS_EXACT."""
         _check(self.lib.llmoe_layer_set_numerics(self.handle, NUMERICS_FAST if fast else NUMERICS_EXACT))
 
     def set_profiling(self, on: bool) -> None:
