@@ -120,6 +120,9 @@ def one_layer_config(llmoe, synth, torch, name, seed, T, mix, shared, pool, step
         "int8_TOPS": 2 * slots * 3 * I * H / t_w / 1e12,
         "stage_ms": prof, "gate_up_bytes": gub, "down_bytes": dnb,
     }
+    res["fast_numerics"] = fast_numerics(llmoe, Gs, fn, steps, warmup, T)
+    for G in Gs:
+        G.forward(x, out=out)
     return res, (Ls[0], Gs, x, out, fn)
 
 
@@ -144,6 +147,18 @@ def norm_step(llmoe, torch, Gs, x, steps, warmup):
         G.forward(x)
     return {"ms_per_step": dt / steps * 1e3, "tokens_per_s": T * steps / dt, "combine_norm_ms": comb,
             "combine_ms": llmoe.time_stage_layers(Gs, "combine", 20)}
+
+
+def fast_numerics(llmoe, Gs, fn, steps, warmup, tokens, layers_per_step=1):
+    """The same step with LLMOE_NUMERICS_FAST (the gate_up SiLU by the hardware transcendentals): step time and the
+    steady-state gate_up duration; the layers are left in exact mode."""
+    for G in Gs:
+        G.set_numerics(True)
+    dt = time_steps(fn, steps, warmup)
+    gu = llmoe.time_stage_layers(Gs, "gate_up", 5)
+    for G in Gs:
+        G.set_numerics(False)
+    return {"ms_per_step": dt / steps * 1e3, "tokens_per_s": tokens * steps / dt, "gate_up_ms": gu}
 
 
 def spot_check(L, out_rows, x_rows, lg_rows, pool):
@@ -194,6 +209,7 @@ def stack_config(llmoe, synth, torch, steps, warmup, nlayers=20, T=2048):
     gu = llmoe.time_stage_layers(Gs, "gate_up", 3)
     dn = llmoe.time_stage_layers(Gs, "down", 3)
     gu_ms, dn_ms = [gu] * nlayers, [dn] * nlayers
+    fast = fast_numerics(llmoe, Gs, fn, steps, warmup, T)
     t_w = (sum(gu_ms) + sum(dn_ms)) * 1e-3
     slots = T * (K + 1) * nlayers
     res = {
@@ -205,7 +221,7 @@ def stack_config(llmoe, synth, torch, steps, warmup, nlayers=20, T=2048):
         "int8_TOPS": 2 * slots * 3 * I * H / t_w / 1e12,
         "int8_mfma_frac_peak": 2 * slots * 3 * I * H / t_w / 1e12 / PEAK_INT8_TOPS,
         "gate_up_ms_per_layer": float(np.mean(gu_ms)), "down_ms_per_layer": float(np.mean(dn_ms)),
-        "spot_check_layer0": check,
+        "spot_check_layer0": check, "fast_numerics": fast,
     }
     for _, G in layers:
         G.close()
@@ -266,6 +282,7 @@ def prefill_config(llmoe, synth, torch, name, T, mix, shared, pool, logits_kind,
     gu = llmoe.time_stage_layers(Gs, "gate_up", 5)
     dn = llmoe.time_stage_layers(Gs, "down", 5)
     topks = [G.read("topk", (T, K), np.int32) for G in Gs]
+    fast = fast_numerics(llmoe, Gs, fn, steps, warmup, T)
     wb = float(np.mean([gate_up_bytes(L, t) + down_bytes(L, t) for L, t in zip(Ls, topks)]))
     slots = T * K + (T if shared else 0)
     t_w = (gu + dn) * 1e-3
@@ -276,7 +293,7 @@ def prefill_config(llmoe, synth, torch, name, T, mix, shared, pool, logits_kind,
             "weight_stream_frac_peak": wb / t_w / 1e9 / PEAK_HBM_GBS,
             "int8_TOPS": 2 * slots * 3 * I * H / t_w / 1e12,
             "int8_mfma_frac_peak": 2 * slots * 3 * I * H / t_w / 1e12 / PEAK_INT8_TOPS, "layers_cycled": nlayers,
-            "spot_check_layer0": check}
+            "spot_check_layer0": check, "fast_numerics": fast}
 
 
 def dense_config(llmoe, synth, torch, R, bits, T, steps, warmup, nmat=40):

@@ -37,6 +37,7 @@ __host__ __device__ constexpr int lds_bytes_for(int K) {
     return (K / GROUP) * (GROUP_B + TILED_NTOK * 8) + TILED_NTOK * 4;
 }
 constexpr int LDS_BYTES = lds_bytes_for(2048);
+constexpr int NXCD = 8;   // XCDs of MI355X (accelerator complex dies, each with its own L2)
 
 template <int I, int N, class F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -426,9 +427,14 @@ template <int MODE>
 __global__ void __launch_bounds__(nthreads_for(MODE == GEMM_DOWN ? 512 : 2048)) tiled_gemm(GemmArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int CMASK = (1 << TASK_RB_SHIFT) - 1;
-    const int s0 = a.tstart[blockIdx.x], s1 = a.tstart[blockIdx.x + 1];
+    // XCD-aware: workgroups are dispatched round-robin over the 8 XCDs, so partition p runs on workgroup
+    // (p % per) * 8 + p / per: each XCD takes a contiguous run of the (chunk-major) task list, and the chunks of a
+    // hot expert -- listed one after another -- share that XCD's L2 for the expert's weights
+    const int G = gridDim.x;
+    const int p = G % NXCD ? int(blockIdx.x) : int(blockIdx.x % NXCD) * (G / NXCD) + int(blockIdx.x / NXCD);
+    const int s0 = a.tstart[p], s1 = a.tstart[p + 1];
     const int c0 = s0 & CMASK, r0 = s0 >> TASK_RB_SHIFT, c1 = s1 & CMASK, r1 = s1 >> TASK_RB_SHIFT;
-    int u = blockIdx.x * 16;   // trace slot (timing builds)
+    int u = p * 16;   // trace slot (timing builds)
     for (int c = c0; c < c1 || (c == c1 && r1 > 0); ++c) {
         const Item it = a.items[c];
         const int bits = a.bits[it.expert];
