@@ -9,7 +9,9 @@
 // Work decomposition (one work item = up to 16*NT slots of ONE expert, so the expert's weights stream from HBM
 // once per item): grid (row blocks, items); a workgroup = 4 waves; wave w owns SPW consecutive 16-row strips and
 // streams them through a register ring (dwordx4 loads, 1 KiB contiguous per wave and load). The item's B rows
-// (int8 activations + per-group scales and sums) are staged once per workgroup in LDS.
+// (int8 activations + per-group scales and sums) are staged once per workgroup in LDS. Each superblock's scales
+// and zeros travel with its codes through the ring (one dword per lane) and reach the lanes through a 192-byte LDS
+// slot of the wave, so the LDS holds no per-strip meta (36 KiB per workgroup at 16 tokens and K = 2048).
 //   gate_up (MODE 0): rows 2I = 1024, K = H = 2048; out Z[slot, i] = fp16(SiLU(g_i) u_i)
 //                     (engine/moe_i8.cu:219-221)
 //   down    (MODE 1): rows H = 2048, K = I = 512; out Y[slot, h] = w_slot acc (engine/moe_i8.cu:222-231)
@@ -36,14 +38,16 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 template <int BITS>
-struct Step {               // the code bytes of one strip-superblock held by one lane (meta comes from LDS)
+struct Step {               // one strip-superblock as held by one lane: code bytes, and dword `lane` of its meta
     u4 c[BITS];
+    uint32_t m;             // lanes 0 .. 47: the 192 meta bytes (scales, zeros), passed on through the wave's LDS slot
 };
 
 template <int BITS>
 __device__ __forceinline__ void load_step(const uint8_t* sbp, int lane, Step<BITS>& r) {
 #pragma unroll
     for (int i = 0; i < BITS; ++i) r.c[i] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(sbp + i * 1024) + lane);
+    if (lane < META_SB / 4) r.m = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(sbp + BITS * 1024) + lane);
 }
 
 __device__ __forceinline__ uint32_t wsel(const u4& v, int i) { return v[i]; }
@@ -110,18 +114,20 @@ struct Geo {
     static constexpr int SPW_MAX = spw<2>();
 };
 
-// ring depth (superblock steps in flight per wave), a divisor of 4. Registers hold only code bytes (the
-// group scales and zeros are staged in LDS), so a wave keeps 4 steps -- 8 to 16 KiB -- in flight.
+// ring depth (superblock steps in flight per wave), a divisor of 4: a wave keeps 4 steps -- 8 to 16 KiB -- in
+// flight (2 of 8-bit codes). The layer GEMMs are built for 3 waves per SIMD (168 VGPRs): measured at 32 tokens
+// against 2 (gate_up 32.0 -> 29.1 us) and 4 (which needs a ring of 2 steps and spills: 30.7 us, down 17.5 ->
+// 20.4 us).
 template <int BITS>
 struct Ring {
     static constexpr int D = BITS == 8 ? 2 : 4;
 };
 
-// LDS: B rows [ntok][K + 16], B scales and sums [K/128][ntok] x 2, then the meta of the workgroup's
-// superblocks [strip][superblock][192 B]
+// LDS: B rows [ntok][K + 16], B scales and sums [K/128][ntok] x 2, then one 192-byte meta slot per wave (the
+// current superblock's scales and zeros, written from the ring and read back per lane quad)
 __host__ __device__ constexpr int b_bytes(int ntok, int K) { return ntok * (K + 16) + ntok * (K / GROUP) * 8; }
 template <int MODE>
-__host__ __device__ constexpr int meta_bytes() { return WAVES * Geo<MODE>::SPW_MAX * Geo<MODE>::NSB * META_SB; }
+__host__ __device__ constexpr int meta_bytes() { return WAVES * META_SB; }
 template <int MODE, int NT>
 __host__ __device__ constexpr int lds_bytes() {
     return b_bytes(16 * NT, Geo<MODE>::NSB * SB_K) + meta_bytes<MODE>() + 16 * NT * 4;   // + the B row table
@@ -146,24 +152,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
     for (int u = 0; u < D; ++u)
         if (u < NSTEP) load_step<BITS>(mat + size_t(u) * SBB, lane, ring[u]);
 
-    // meta (scales, zeros) of every superblock of the workgroup's strips -> LDS
+    // this wave's meta slot
     uint8_t* meta_lds = lds + b_bytes(NTOK, K);
-    {
-        constexpr int NMETA = WAVES * SPW * NSB * (META_SB / 16);   // 16-byte chunks
-        constexpr int PM = (NMETA + WAVES * 64 - 1) / (WAVES * 64);
-        const uint8_t* wg_mat = a.base + a.off[it.expert] + size_t(row_block * WAVES * SPW) * NSB * SBB;
-        u4 mv[PM];
-#pragma unroll
-        for (int i = 0; i < PM; ++i) {
-            const int idx = threadIdx.x + i * WAVES * 64;
-            if (idx < NMETA) mv[i] = *reinterpret_cast<const u4*>(wg_mat + size_t(idx / 12) * SBB + BITS * 1024 + 16 * (idx % 12));
-        }
-#pragma unroll
-        for (int i = 0; i < PM; ++i) {
-            const int idx = threadIdx.x + i * WAVES * 64;
-            if (idx < NMETA) *reinterpret_cast<u4*>(meta_lds + 16 * idx) = mv[i];
-        }
-    }
+    uint8_t* mp = meta_lds + wave * META_SB;
 
     // stage the item's B rows in LDS: q8 rows [NTOK][LDQ], scales [G][NTOK], sums [G][NTOK]
     int8_t* bq = reinterpret_cast<int8_t*>(lds);
@@ -235,7 +226,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
         Step<BITS>& cur = ring[u % D];
         constexpr int sb = u % NSB;
         const int strip = strip0 + u / NSB;
-        const uint8_t* mp = meta_lds + (size_t(strip - row_block * WAVES * SPW) * NSB + sb) * META_SB;
+        if (lane < META_SB / 4) *reinterpret_cast<uint32_t*>(mp + 4 * lane) = cur.m;
         const u4 ms0 = *reinterpret_cast<const u4*>(mp + 32 * q);
         const u4 ms1 = *reinterpret_cast<const u4*>(mp + 32 * q + 16);
         const u4 zw4 = *reinterpret_cast<const u4*>(mp + 128 + 16 * q);
@@ -381,7 +372,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
 // Persistent: the grid is the number of workgroups that fit the GPU at once; each workgroup takes the work units
 // blockIdx.x, blockIdx.x + gridDim.x, ... (units are ordered heaviest first, so the long ones start first).
 template <int MODE, int NT>
-__global__ void __launch_bounds__(WAVES * 64) expert_gemm(GemmArgs a) {
+__global__ void __launch_bounds__(WAVES * 64, NT == 1 ? 3 : 1) expert_gemm(GemmArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int n = *a.n_items;
     for (int u = blockIdx.x; u < n; u += gridDim.x) {
