@@ -7,18 +7,6 @@ namespace llmoe {
 
 namespace {
 
-__device__ __forceinline__ float group16_max(float m) {
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, xor_lane(m, o));
-    return m;
-}
-__device__ __forceinline__ int group16_sum(int v) {
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) v += xor_lane(v, o);
-    return v;
-}
-__device__ __forceinline__ int clamp127(float r) { return int(fminf(fmaxf(r, -127.0f), 127.0f)); }
-
 // A8 of rows of fp32 (engine/ops.cu:42-66): s = max(max|v| / 127, 1e-30), q = clamp(rint(v / s), +-127).
 // One wave per 512 columns of one row; grid (cols/512/4 rounded up, rows), 256 threads.
 __global__ void __launch_bounds__(256) quant_a8_kernel(const float* __restrict__ x, int rows, int cols,
@@ -54,59 +42,19 @@ __global__ void __launch_bounds__(256) quant_a8_kernel(const float* __restrict__
     }
 }
 
-// Z' = A8(Z H512 / sqrt(512)) per slot (engine/moe_i8.cu:447-502). One wave per slot, lane l owns values
-// 8l .. 8l+7: butterfly stages h = 1, 2, 4 in registers, h = 8 .. 256 by lane shuffles (xor 1 .. 32), in
-// ascending h. The group quantiser multiplies by 1/s. Logical order out. grid ceil(n/4), 256 threads.
+// Z' = A8(Z H512 / sqrt(512)) per slot (engine/moe_i8.cu:447-502), one wave per slot (fwht512_a8).
+// grid ceil(n/4), 256 threads.
 __global__ void __launch_bounds__(256) fwht_a8_kernel(const uint16_t* __restrict__ Z, int nslots,
                                                       int8_t* __restrict__ q, float* __restrict__ s,
                                                       int* __restrict__ sum) {
     const int lane = threadIdx.x & 63;
     const int slot = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (slot >= nslots) return;
-    const uint4 raw = *reinterpret_cast<const uint4*>(Z + size_t(slot) * 512 + 8 * lane);
-    const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
-    float x[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        x[2 * j] = f16_bits_to_f32(rw[j] & 0xFFFFu);
-        x[2 * j + 1] = f16_bits_to_f32(rw[j] >> 16);
-    }
-#pragma unroll
-    for (int h = 1; h < 8; h <<= 1)
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (!(j & h)) {
-                const float a = x[j], b = x[j + h];
-                x[j] = a + b;
-                x[j + h] = a - b;
-            }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        // butterfly: the lower lane of the pair keeps x + y, the upper y - x; fma(+-1, x, y) rounds exactly
-        // like that sum or difference
-        const float sg = (lane & o) ? -1.0f : 1.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = __builtin_fmaf(sg, x[j], xor_lane(x[j], o));
-    }
-    float m = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        x[j] = x[j] * 0.04419417382415922f;
-        m = fmaxf(m, fabsf(x[j]));
-    }
-    m = group16_max(m);
-    const float sc = fmaxf(m / 127.0f, 1e-30f), inv = 1.0f / sc;
-    int tot = 0;
-    uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int qq = clamp127(__builtin_rintf(x[j] * inv));
-        tot += qq;
-        if (j < 4) w0 |= uint32_t(qq & 0xFF) << (8 * j);
-        else w1 |= uint32_t(qq & 0xFF) << (8 * (j - 4));
-    }
-    *reinterpret_cast<uint2*>(q + size_t(slot) * 512 + 8 * lane) = make_uint2(w0, w1);
-    tot = group16_sum(tot);
+    uint2 qw;
+    float sc;
+    int tot;
+    fwht512_a8(Z + size_t(slot) * 512, lane, qw, sc, tot);
+    *reinterpret_cast<uint2*>(q + size_t(slot) * 512 + 8 * lane) = qw;
     if ((lane & 15) == 0) {
         s[size_t(slot) * 4 + (lane >> 4)] = sc;
         sum[size_t(slot) * 4 + (lane >> 4)] = tot;

@@ -455,7 +455,8 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     HIPCHECK(launch_gemm(GEMM_GATE_UP, g, tg, L->tiled, st));
     L->mark(LLMOE_STAGE_GATE_UP, true, st);
     L->mark(LLMOE_STAGE_FWHT, false, st);
-    HIPCHECK(launch_fwht_a8(w.Z, S, w.zq, w.zs, w.zsum, st));
+    // FWHT-512 + A8 of Z: its own kernel before the tiled down GEMM; the streamed down GEMM stages it per item
+    if (L->tiled) HIPCHECK(launch_fwht_a8(w.Z, S, w.zq, w.zs, w.zsum, st));
     L->mark(LLMOE_STAGE_FWHT, true, st);
     // down: B rows are slot rows of Z'
     g.items = L->units_dn;
@@ -466,6 +467,7 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     g.K = I; g.R = H; g.Z = nullptr; g.Y = w.Y;
     g.fast = 0;
     tg = g;
+    g.zin = w.Z; g.xq_out = w.zq; g.xs_out = w.zs; g.xsum_out = w.zsum;
     tg.items = L->tunits_dn;
     tg.tstart = L->tstart + L->g_gu + 1;
     tg.n_items = L->n_units + 3;

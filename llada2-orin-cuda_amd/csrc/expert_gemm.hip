@@ -161,7 +161,32 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
     float* bs = reinterpret_cast<float*>(lds + NTOK * LDQ);
     int* bsum = reinterpret_cast<int*>(bs + G * NTOK);
     const int ntok = it.ntok;
-    {
+    if (MODE == GEMM_DOWN && a.zin != nullptr) {
+        // B rows = A8(FWHT-512(Z)) of the item's slots, one wave per slot (the operations of fwht_a8_kernel); the
+        // units of row block 0 also store them for the buffers' readers. Rows n >= ntok are zero.
+#pragma unroll 1
+        for (int n = wave; n < NTOK; n += WAVES) {
+            uint2 qw = make_uint2(0u, 0u);
+            float sc = 0.0f;
+            int tot = 0;
+            if (n < ntok) {
+                const size_t slot = size_t(it.slot0 + n);
+                fwht512_a8(a.zin + slot * K, lane, qw, sc, tot);
+                if (row_block == 0) {
+                    *reinterpret_cast<uint2*>(a.xq_out + slot * K + 8 * lane) = qw;
+                    if ((lane & 15) == 0) {
+                        a.xs_out[slot * G + (lane >> 4)] = sc;
+                        a.xsum_out[slot * G + (lane >> 4)] = tot;
+                    }
+                }
+            }
+            *reinterpret_cast<uint2*>(bq + n * LDQ + 8 * lane) = qw;
+            if ((lane & 15) == 0) {
+                bs[(lane >> 4) * NTOK + n] = sc;
+                bsum[(lane >> 4) * NTOK + n] = -tot;   // negated: C = zero * (-sum)
+            }
+        }
+    } else {
         // B rows through a row table in LDS (one round of slot_token loads), then NTOK * K / 16 chunks of 16
         // bytes over 256 threads at clamped rows, all issued before the LDS stores
         int* rowtab = reinterpret_cast<int*>(meta_lds + meta_bytes<MODE>());

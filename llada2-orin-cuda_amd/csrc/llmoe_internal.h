@@ -182,6 +182,70 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
 }
 
+__device__ __forceinline__ float group16_max(float m) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, xor_lane(m, o));
+    return m;
+}
+__device__ __forceinline__ int group16_sum(int v) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) v += xor_lane(v, o);
+    return v;
+}
+__device__ __forceinline__ int clamp127(float r) { return int(fminf(fmaxf(r, -127.0f), 127.0f)); }
+
+// Z' = A8(Z H512 / sqrt(512)) of one fp16 row of 512 values by one wave (engine/moe_i8.cu:447-502): lane l owns
+// values 8l .. 8l+7; butterfly stages h = 1, 2, 4 in registers, h = 8 .. 256 by lane shuffles (xor 1 .. 32), in
+// ascending h; the group quantiser multiplies by 1/s. Out (logical order): the lane's 8 codes, and its group's
+// scale and code sum (group = lane / 16). All 64 lanes must be active.
+__device__ __forceinline__ void fwht512_a8(const uint16_t* __restrict__ zrow, int lane, uint2& qw, float& sc, int& tot) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(zrow + 8 * lane);
+    const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        x[2 * j] = f16_bits_to_f32(rw[j] & 0xFFFFu);
+        x[2 * j + 1] = f16_bits_to_f32(rw[j] >> 16);
+    }
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (!(j & h)) {
+                const float a = x[j], b = x[j + h];
+                x[j] = a + b;
+                x[j + h] = a - b;
+            }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        // butterfly: the lower lane of the pair keeps x + y, the upper y - x; fma(+-1, x, y) rounds exactly
+        // like that sum or difference
+        const float sg = (lane & o) ? -1.0f : 1.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = __builtin_fmaf(sg, x[j], xor_lane(x[j], o));
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        x[j] = x[j] * 0.04419417382415922f;
+        m = fmaxf(m, fabsf(x[j]));
+    }
+    m = group16_max(m);
+    sc = fmaxf(m / 127.0f, 1e-30f);
+    const float inv = 1.0f / sc;
+    int t = 0;
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int qq = clamp127(__builtin_rintf(x[j] * inv));
+        t += qq;
+        if (j < 4) w0 |= uint32_t(qq & 0xFF) << (8 * j);
+        else w1 |= uint32_t(qq & 0xFF) << (8 * (j - 4));
+    }
+    qw = make_uint2(w0, w1);
+    tot = group16_sum(t);
+}
+
 // ---- host launchers (each returns the launch's hipError_t) ----
 
 struct GemmArgs {
@@ -203,6 +267,12 @@ struct GemmArgs {
     const int* tstart;          // tiled: [G + 1] first task of each workgroup (the work partition above)
     int accumulate;             // GEMM_DENSE: Y += acc instead of Y = acc
     int fast;                   // gate_up: SiLU by the hardware exp / reciprocal and fp16 conversion
+    // streamed down GEMM: with zin set, the B rows are staged as A8(FWHT-512(zin[slot])) instead of read from xq / xs /
+    // xsum, and the units of row block 0 also write those rows to xq_out / xs_out / xsum_out
+    const uint16_t* zin;
+    int8_t* xq_out;
+    float* xs_out;
+    int* xsum_out;
 };
 
 // GEMM_DENSE: a plain W.A8 projection [R, 2048] (rows in packlib order), out Y[token, r] = acc (or += acc)
