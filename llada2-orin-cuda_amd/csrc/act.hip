@@ -61,30 +61,31 @@ __global__ void __launch_bounds__(256) fwht_a8_kernel(const uint16_t* __restrict
     }
 }
 
-// out[t, :] = sum_{k < kk} Y[tok_slots[t, k], :], k ascending (engine/moe_i8.cu:505-515). grid T, 256 threads.
+// out[t, :] = sum_{k < kk} Y[tok_slots[t, k], :], k ascending (engine/moe_i8.cu:505-515). grid (T, column slices).
 constexpr int MAX_KK = 9;   // top-8 + the shared expert
 __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ Y, const int* __restrict__ tok_slots,
                                                       int H, int kk, int K1, float* __restrict__ out) {
     const int t = blockIdx.x;
+    // columns [h0, h1) of the row: gridDim.y slices, so that a small T still spreads over many CUs
+    const int hw = H / int(gridDim.y), h0 = int(blockIdx.y) * hw, h1 = h0 + hw;
     int sl[MAX_KK];
 #pragma unroll
     for (int k = 0; k < MAX_KK; ++k) sl[k] = k < kk ? tok_slots[t * K1 + k] : 0;
-    // R float4 columns per thread per pass (a whole 2048-wide row at 256 threads): every load of the pass is in
-    // flight before the ordered sums
+    // R float4 columns per thread per pass: every load of the pass is in flight before the ordered sums
     constexpr int R = 2;
-    for (int hb = threadIdx.x * 4; hb < H; hb += blockDim.x * 4 * R) {
+    for (int hb = h0 + threadIdx.x * 4; hb < h1; hb += blockDim.x * 4 * R) {
         float4 v[R][MAX_KK];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int h = hb + r * blockDim.x * 4;
 #pragma unroll
             for (int k = 0; k < MAX_KK; ++k)
-                if (k < kk && h < H) v[r][k] = *reinterpret_cast<const float4*>(Y + size_t(sl[k]) * H + h);
+                if (k < kk && h < h1) v[r][k] = *reinterpret_cast<const float4*>(Y + size_t(sl[k]) * H + h);
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int h = hb + r * blockDim.x * 4;
-            if (h >= H) break;
+            if (h >= h1) break;
             float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
             for (int k = 0; k < MAX_KK; ++k) {
@@ -254,7 +255,9 @@ hipError_t launch_combine_norm(const float* Y, const int* tok_slots, int T, int 
 hipError_t launch_combine(const float* Y, const int* tok_slots, int T, int H, int kk, int K1, float* out,
                           hipStream_t st) {
     if (T <= 0) return hipSuccess;
-    combine_kernel<<<T, 256, 0, st>>>(Y, tok_slots, H, kk, K1, out);
+    // a decode step's few rows are split over 8 column slices (256 columns, one pass of 64 threads x 2 float4)
+    const int ns = T <= 256 && H % 256 == 0 ? H / 256 : 1;
+    combine_kernel<<<dim3(T, ns), ns > 1 ? 64 : 256, 0, st>>>(Y, tok_slots, H, kk, K1, out);
     return hipGetLastError();
 }
 

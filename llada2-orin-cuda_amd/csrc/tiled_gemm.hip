@@ -412,10 +412,8 @@ template <int BITS, int MODE, int NTILE>
 __device__ __forceinline__ void tiled_body(const GemmArgs& a, const Item& it, uint8_t* lds, int rb0, int rb1, int u) {
     constexpr int K = MODE == GEMM_DOWN ? 512 : 2048;
     (void)u;
-    // the expert's matrix, wave-uniform (one load per unit, not one per row block)
-    const uint64_t mo = a.off[it.expert];
-    const uint8_t* mat = a.base + ((uint64_t(__builtin_amdgcn_readfirstlane(uint32_t(mo >> 32))) << 32) |
-                                   __builtin_amdgcn_readfirstlane(uint32_t(mo)));
+    // the expert's matrix (one load per unit, not one per row block; the compiler keeps it wave-uniform)
+    const uint8_t* mat = a.base + a.off[it.expert];
     stage_chunk<K>(a, it, lds);
     TRACE_AT(u, 1);
     for (int rb = rb0; rb < rb1; ++rb) tiled_rowblock<BITS, MODE, NTILE>(a, it, mat, lds, rb);
