@@ -395,7 +395,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
 }
 
 // Persistent: the grid is the number of workgroups that fit the GPU at once; each workgroup takes the work units
-// blockIdx.x, blockIdx.x + gridDim.x, ... (units are ordered heaviest first, so the long ones start first).
+// blockIdx.x, blockIdx.x + gridDim.x, ... (units are ordered longest first, so the long ones start first).
+// Measured at 32 tokens and not kept: units claimed from a device counter as workgroups become free (0.0625 ->
+// 0.073 ms per step: same-address device-scope atomics serialise across the 8 XCDs), and a second round assigned
+// in reverse (0.0610 -> 0.0631 ms).
 template <int MODE, int NT>
 __global__ void __launch_bounds__(WAVES * 64, NT == 1 ? 3 : 1) expert_gemm(GemmArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];

@@ -152,6 +152,10 @@ __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int o) {
 }
 
 __device__ __forceinline__ int width_class(int bits) { return bits == 8 ? 0 : bits == 4 ? 1 : bits == 3 ? 2 : 3; }
+// decode units, longest first: a streamed unit's time is set by its vector work, and the 2-bit units (4 strips per
+// wave) have the most tiles (measured at 32 tokens against the byte order 8, 4, 3, 2 with the shared expert first:
+// 0.0623 -> 0.0615 ms per step)
+__device__ __forceinline__ int decode_class(int bits) { return bits == 2 ? 0 : bits == 3 ? 1 : bits == 4 ? 2 : 3; }
 
 // the units of expert e: items of <= ntok of its c slots starting at slot st, each split into row blocks
 __device__ void emit_units(int e, int c, int st, int ntok, int bits, int base_gu, int base_dn, Item* units_gu,
@@ -276,7 +280,7 @@ __device__ unsigned long long g_plan_trace[16];
 #endif
 
 // Slots: expert-major, token-ascending; shared slots T K + t. Units: items of 16 slots split into row blocks by
-// code width, heaviest first (the shared expert, then 8 / 4 / 3 / 2-bit experts).
+// code width, longest first (2 / 3 / 4 / 8-bit experts, then the shared expert).
 __global__ void __launch_bounds__(256) dispatch_kernel(int T, int E, int K, const int* __restrict__ topk,
                                                        const float* __restrict__ topw, DecodeState ds, DispatchOut d) {
     __shared__ uint32_t m_s[MAXE];
@@ -294,7 +298,7 @@ __global__ void __launch_bounds__(256) dispatch_kernel(int T, int E, int K, cons
     const int c = __popc(m);
     const int bw = e < E ? d.bits[e] : 2;
     const int nit = (c + 15) >> 4;
-    const int cls = width_class(bw);
+    const int cls = decode_class(bw);
     const uint64_t vg = uint64_t(nit * gemm_row_blocks(false, bw)) << (16 * cls);
     const uint64_t vd = uint64_t(nit * gemm_row_blocks(true, bw)) << (16 * cls);
     int incl = c;
@@ -326,8 +330,8 @@ __global__ void __launch_bounds__(256) dispatch_kernel(int T, int E, int K, cons
     const int sbits = d.has_shared ? d.bits[E] : 8;
     const int ns = d.has_shared ? (T + 15) >> 4 : 0;
     const int srg = gemm_row_blocks(false, sbits), srd = gemm_row_blocks(true, sbits);
-    // class bases: shared units first, then classes 0 .. 3
-    int bg = ns * srg, bd = ns * srd, og = 0, od = 0;
+    // class bases: classes 0 .. 3, then the shared expert's units
+    int bg = 0, bd = 0, og = 0, od = 0;
     for (int k = 0; k < 4; ++k) {
         if (k == cls) {
             og = bg + int(((ig - vg) >> (16 * k)) & 0xFFFFu);
@@ -346,11 +350,11 @@ __global__ void __launch_bounds__(256) dispatch_kernel(int T, int E, int K, cons
             for (int r = 0; r < rd; ++r) d.units_dn[od + j * rd + r] = Item{e, s0, n, r};
         }
     }
-    for (int u = e; u < ns * srg; u += 256) units_shared(d.units_gu, u, srg, E, T, K);
-    for (int u = e; u < ns * srd; u += 256) units_shared(d.units_dn, u, srd, E, T, K);
+    for (int u = e; u < ns * srg; u += 256) units_shared(d.units_gu + bg, u, srg, E, T, K);
+    for (int u = e; u < ns * srd; u += 256) units_shared(d.units_dn + bd, u, srd, E, T, K);
     if (e == 0) {
-        d.n_units[0] = bg;
-        d.n_units[1] = bd;
+        d.n_units[0] = bg + ns * srg;
+        d.n_units[1] = bd + ns * srd;
         d.n_units[2] = 0;
         d.n_units[3] = 0;
     }
