@@ -178,7 +178,10 @@ __device__ __forceinline__ void stage_chunk(const GemmArgs& a, const Item& it, u
     constexpr int G = K / GROUP, PER = TILED_NTOK * (K / 16) / NTHREADS;
     constexpr int PS = (G * TILED_NTOK + NTHREADS - 1) / NTHREADS;
     static_assert(PER * NTHREADS == TILED_NTOK * (K / 16) && TILED_NTOK == 64, "staging split");
-    const int tid = threadIdx.x;
+    // the staging addresses are recomputed per chunk (a few VALU): hoisted out of the chunk loop they would stay
+    // live across every row block and be spilled
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
     float* ss = reinterpret_cast<float*>(lds + G * GROUP_B);
     int* sq = reinterpret_cast<int*>(ss + G * TILED_NTOK);
     int* rowtab = sq + G * TILED_NTOK;
