@@ -231,35 +231,59 @@ __device__ __forceinline__ void stage_chunk(const GemmArgs& a, const Item& it, u
     __syncthreads();
 }
 
-// One row block: wave w computes strips (rb * NW + w) * S .. + S - 1 for the chunk staged in LDS.
+// 4-bit codes subtract the zero while unpacking once the unpacked tile serves two or more token tiles (16 VALU per
+// tile against 8 per token tile for the accumulator's zero term)
+template <int BITS, int NTILE>
+__host__ __device__ constexpr bool zacc() { return BITS == 8 || (BITS == 4 && NTILE == 1); }
+
+// The weight registers of one row block (wave w's strips (rb * NW + w) * S .. + S - 1): the first superblock's
+// codes and meta, and the second superblock's meta for K = 2048
+template <int BITS, int MODE>
+struct RowRegs {
+    static constexpr int S = tiled_spw(MODE == GEMM_DOWN, BITS);
+    Codes<BITS> cd[S];
+    Late lt[2][S];
+};
+
 template <int BITS, int MODE, int NTILE>
-__device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it, const uint8_t* mat,
-                                               const uint8_t* lds, int rb) {
+__device__ __forceinline__ void rowblock_load(const uint8_t* mat, int rb, RowRegs<BITS, MODE>& r) {
+    constexpr int NSB = MODE == GEMM_DOWN ? 1 : 4, S = RowRegs<BITS, MODE>::S, NW = nw_for(NSB * SB_K);
+    constexpr size_t SBB = sb_bytes(BITS);
+    constexpr bool ZACC = zacc<BITS, NTILE>();
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint8_t* p0 = mat + size_t((rb * NW + wave) * S) * NSB * SBB;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const uint8_t* p = p0 + size_t(s) * NSB * SBB;
+#pragma unroll
+        for (int i = 0; i < Codes<BITS>::N; ++i) load_code<BITS>(p, lane, i, r.cd[s]);
+        load_s0<BITS>(p, lane, r.cd[s]);
+        load_late<BITS, ZACC>(p, lane, r.lt[0][s]);
+        if constexpr (NSB > 1) load_late<BITS, ZACC>(p + SBB, lane, r.lt[1][s]);
+    }
+}
+
+// One row block's products for the chunk staged in LDS, from the registers rowblock_load filled (the later
+// superblocks of K = 2048 are requested along the way): the fp32 accumulators of the wave's (strip, token tile)
+// pairs.
+template <int BITS, int MODE, int NTILE>
+__device__ __forceinline__ void rowblock_compute(const uint8_t* mat, const uint8_t* lds, int rb,
+                                                 RowRegs<BITS, MODE>& r,
+                                                 float (&acc)[RowRegs<BITS, MODE>::S][NTILE][4]) {
     constexpr bool DOWN = MODE == GEMM_DOWN;
     constexpr int NSB = DOWN ? 1 : 4, K = NSB * SB_K, G = K / GROUP;
-    constexpr int S = tiled_spw(DOWN, BITS), NW = nw_for(K);
+    constexpr int S = RowRegs<BITS, MODE>::S, NW = nw_for(K);
     constexpr size_t SBB = sb_bytes(BITS);
-    // 4-bit codes subtract the zero while unpacking once the unpacked tile serves two or more token tiles (16 VALU
-    // per tile against 8 per token tile for the accumulator's zero term)
-    constexpr bool ZACC = BITS == 8 || (BITS == 4 && NTILE == 1);
+    constexpr bool ZACC = zacc<BITS, NTILE>();
     const int lane = threadIdx.x & 63, q = lane >> 4, col = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int strip0 = (rb * NW + wave) * S;
     auto sbp = [&](int s, int sb) { return mat + (size_t(strip0 + s) * NSB + sb) * SBB; };
     const float* ss = reinterpret_cast<const float*>(lds + G * GROUP_B);
     const int* sq = reinterpret_cast<const int*>(ss + G * TILED_NTOK);
-
-    Codes<BITS> cd[S];
-    Late lt[2][S];
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-#pragma unroll
-        for (int i = 0; i < Codes<BITS>::N; ++i) load_code<BITS>(sbp(s, 0), lane, i, cd[s]);
-        load_s0<BITS>(sbp(s, 0), lane, cd[s]);
-        load_late<BITS, ZACC>(sbp(s, 0), lane, lt[0][s]);
-        if constexpr (NSB > 1) load_late<BITS, ZACC>(sbp(s, 1), lane, lt[1][s]);
-    }
-    float acc[S][NTILE][4];
+    Codes<BITS> (&cd)[S] = r.cd;
+    Late (&lt)[2][S] = r.lt;
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
@@ -362,7 +386,16 @@ __device__ __forceinline__ void tiled_rowblock(const GemmArgs& a, const Item& it
         });
     });
 
-    // fused epilogue
+}
+
+// The row block's fused epilogue: Z = fp16(SiLU(g) u) (gate_up), Y = w acc (down) or Y (+)= acc (dense).
+template <int BITS, int MODE, int NTILE>
+__device__ __forceinline__ void rowblock_store(const GemmArgs& a, const Item& it, int rb,
+                                               const float (&acc)[RowRegs<BITS, MODE>::S][NTILE][4]) {
+    constexpr int S = RowRegs<BITS, MODE>::S, NW = nw_for(MODE == GEMM_DOWN ? SB_K : 4 * SB_K);
+    const int lane = threadIdx.x & 63, q = lane >> 4, col = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int strip0 = (rb * NW + wave) * S;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int strip = strip0 + s;
@@ -417,9 +450,22 @@ __device__ __forceinline__ void tiled_body(const GemmArgs& a, const Item& it, ui
     (void)u;
     // the expert's matrix (one load per unit, not one per row block; the compiler keeps it wave-uniform)
     const uint8_t* mat = a.base + a.off[it.expert];
+    // row block rb + 1's first weights are requested between rb's products and rb's stores: the weight loads then
+    // precede the output stores in the in-order memory counter, so waiting for them never waits for the stores
+    RowRegs<BITS, MODE> r;
+    rowblock_load<BITS, MODE, NTILE>(mat, rb0, r);
     stage_chunk<K>(a, it, lds);
     TRACE_AT(u, 1);
-    for (int rb = rb0; rb < rb1; ++rb) tiled_rowblock<BITS, MODE, NTILE>(a, it, mat, lds, rb);
+    for (int rb = rb0; rb < rb1; ++rb) {
+        float acc[RowRegs<BITS, MODE>::S][NTILE][4];
+        rowblock_compute<BITS, MODE, NTILE>(mat, lds, rb, r, acc);
+        // (8-bit codes of the 16-wave down GEMM: the accumulators and a whole superblock of codes do not fit the
+        // registers together, so the stores go first)
+        constexpr bool LOAD_FIRST = !(MODE == GEMM_DOWN && BITS == 8);
+        if (LOAD_FIRST && rb + 1 < rb1) rowblock_load<BITS, MODE, NTILE>(mat, rb + 1, r);
+        rowblock_store<BITS, MODE, NTILE>(a, it, rb, acc);
+        if (!LOAD_FIRST && rb + 1 < rb1) rowblock_load<BITS, MODE, NTILE>(mat, rb + 1, r);
+    }
 }
 
 // Workgroup w runs the row-block tasks tstart[w] .. tstart[w + 1] (chunk-major, so the chunk's activations are
