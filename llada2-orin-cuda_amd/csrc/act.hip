@@ -15,31 +15,9 @@ __global__ void __launch_bounds__(256) quant_a8_kernel(const float* __restrict__
     const int lane = threadIdx.x & 63;
     const int chunk = blockIdx.x * 4 + (threadIdx.x >> 6), row = blockIdx.y;
     if (chunk * 512 >= cols || row >= rows) return;
-    const size_t base = size_t(row) * cols + size_t(chunk) * 512 + 8 * lane;
-    const float4 a = *reinterpret_cast<const float4*>(x + base);
-    const float4 b = *reinterpret_cast<const float4*>(x + base + 4);
-    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    float m = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
-    m = group16_max(m);
-    const float sc = fmaxf(m / 127.0f, 1e-30f);
-    int tot = 0;
-    uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int qq = clamp127(__builtin_rintf(v[j] / sc));
-        tot += qq;
-        if (j < 4) w0 |= uint32_t(qq & 0xFF) << (8 * j);
-        else w1 |= uint32_t(qq & 0xFF) << (8 * (j - 4));
-    }
-    *reinterpret_cast<uint2*>(q + base) = make_uint2(w0, w1);
-    tot = group16_sum(tot);
-    if ((lane & 15) == 0) {
-        const size_t gi = size_t(row) * (cols / GROUP) + size_t(chunk) * 4 + (lane >> 4);
-        s[gi] = sc;
-        sum[gi] = tot;
-    }
+    const size_t base = size_t(row) * cols + size_t(chunk) * 512;
+    const size_t gi = size_t(row) * (cols / GROUP) + size_t(chunk) * 4;
+    quant_a8_512(x + base, lane, q + base, s + gi, sum + gi);
 }
 
 // Z' = A8(Z H512 / sqrt(512)) per slot (engine/moe_i8.cu:447-502), one wave per slot (fwht512_a8).

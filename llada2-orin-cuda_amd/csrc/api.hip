@@ -366,8 +366,10 @@ int llmoe_quantize_a8(const float* x, int rows, int cols, int8_t* q, float* s, i
 }  // extern "C"
 
 namespace {
-// routing; with quant set (and x given) the router kernel also writes the A8 of x into the layer workspace
-int route_impl(llmoe_layer* L, const float* x, const float* logits, int T, hipStream_t st, bool quant) {
+// routing; with quant set (and x given) the router kernel also writes the A8 of x into the layer workspace; with
+// xa8 set (routing from logits) the first per-token routing kernel writes the A8 of xa8 there
+int route_impl(llmoe_layer* L, const float* x, const float* logits, int T, hipStream_t st, bool quant,
+               const float* xa8 = nullptr) {
     const auto& d = L->d;
     L->routed_T = -1;
     if (int rc = prepare_items(L, T)) return rc;
@@ -382,18 +384,19 @@ int route_impl(llmoe_layer* L, const float* x, const float* logits, int T, hipSt
         part = L->part;
         nchunks = ROUTER_KC;
     }
+    const QuantX qx{x ? nullptr : xa8, L->xq, L->xs, L->xsum};
     L->mark(LLMOE_STAGE_ROUTE, false, st);
     if (T <= d.block) {   // one routing block (a decode step): route, plan and place in one workgroup
         HIPCHECK(launch_decode_route(part, nchunks, L->bias, T, d.n_experts, d.top_k, d.pool, d.routed_scale, L->sig,
                                      L->topk, L->topw, L->blockmax, L->tmask, d.has_shared, L->bits_d,
                                      L->count, L->start, L->units_gu, L->units_dn, L->n_units, L->slot_token,
-                                     L->slot_weight, L->tok_slots, st));
+                                     L->slot_weight, L->tok_slots, qx, st));
         L->mark(LLMOE_STAGE_ROUTE, true, st);
         L->routed_T = T;
         return LLMOE_OK;
     }
     HIPCHECK(launch_route(part, nchunks, L->bias, T, d.n_experts, d.top_k, d.pool, d.block, d.routed_scale, L->sig,
-                          L->blockmax, L->topk, L->topw, L->mask, st));
+                          L->blockmax, L->topk, L->topw, L->mask, qx, st));
     L->mark(LLMOE_STAGE_ROUTE, true, st);
     return plan_and_place(L, L->topk, L->topw, T, st);
 }
@@ -573,13 +576,9 @@ int llmoe_layer_forward(llmoe_layer* L, const float* x, const float* logits, int
     if (int rc = check_T(L, T)) return rc;
     if (!x || !out) return fail(LLMOE_EINVAL, "null argument");
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    if (logits || !L->router_w) {   // A8 on its own; with the router, its kernel quantises x on the way
-        L->mark(LLMOE_STAGE_QUANT, false, st);
-        if (int rc = llmoe_quantize_a8(x, T, L->d.hidden, L->xq, L->xs, L->xsum, stream)) return rc;
-        L->mark(LLMOE_STAGE_QUANT, true, st);
-    }
     if (!logits && !L->router_w) return fail(LLMOE_EINVAL, "layer created without a router matrix");
-    if (int rc = route_impl(L, logits ? nullptr : x, logits, T, st, logits == nullptr)) return rc;
+    // the A8 of x rides on the first routing kernel: the router's (x·Wr) or, from given logits, the per-token one
+    if (int rc = route_impl(L, logits ? nullptr : x, logits, T, st, logits == nullptr, logits ? x : nullptr)) return rc;
     return llmoe_experts(L, L->xq, L->xs, L->xsum, T, out, stream);
 }
 

@@ -246,6 +246,44 @@ __device__ __forceinline__ void fwht512_a8(const uint16_t* __restrict__ zrow, in
     tot = group16_sum(t);
 }
 
+// A8 of 512 consecutive values by one wave (engine/ops.cu:42-66): lane l owns values 8l .. 8l+7, a 128-group is
+// 16 lanes; s = max(max|v| / 127, 1e-30), q = clamp(rint(v / s), +-127). Writes the lane's 8 codes and, from the
+// group's first lane, its scale and code sum (s4 / sum4: the 4 groups of the 512). All 64 lanes must be active.
+__device__ __forceinline__ void quant_a8_512(const float* __restrict__ x, int lane, int8_t* __restrict__ q,
+                                             float* __restrict__ s4, int* __restrict__ sum4) {
+    const float4 a = *reinterpret_cast<const float4*>(x + 8 * lane);
+    const float4 b = *reinterpret_cast<const float4*>(x + 8 * lane + 4);
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
+    m = group16_max(m);
+    const float sc = fmaxf(m / 127.0f, 1e-30f);
+    int tot = 0;
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int qq = clamp127(__builtin_rintf(v[j] / sc));
+        tot += qq;
+        if (j < 4) w0 |= uint32_t(qq & 0xFF) << (8 * j);
+        else w1 |= uint32_t(qq & 0xFF) << (8 * (j - 4));
+    }
+    *reinterpret_cast<uint2*>(q + 8 * lane) = make_uint2(w0, w1);
+    tot = group16_sum(tot);
+    if ((lane & 15) == 0) {
+        s4[lane >> 4] = sc;
+        sum4[lane >> 4] = tot;
+    }
+}
+
+// the A8 of the layer input (H = 2048) done by the first per-token routing kernel when routing from given logits
+struct QuantX {
+    const float* x;     // [T, 2048] fp32, nullptr: no A8
+    int8_t* q;
+    float* s;
+    int* sum;
+};
+
 // ---- host launchers (each returns the launch's hipError_t) ----
 
 struct GemmArgs {
@@ -306,7 +344,7 @@ hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, i
                                 float* qs, int* qsum, hipStream_t st);
 hipError_t launch_route(const float* part, int nchunks, const float* bias, int T, int E, int K, int C, int block,
                         float rscale, float* sig, uint32_t* blockmax, int32_t* topk, float* topw, uint32_t* mask,
-                        hipStream_t st);
+                        const QuantX& qx, hipStream_t st);
 // decode step (T <= 32, one routing block): [scores and pool keys (pool < E)], selection in ceil(T/8)
 // workgroups, then one workgroup builds the slots and work units (streamed, 16 slots per item). blockmax / tmask
 // [E] must be zero on entry and are zero again on exit. sig: [T, E] scratch.
@@ -314,7 +352,7 @@ hipError_t launch_decode_route(const float* part, int nchunks, const float* bias
                                float rscale, float* sig, int32_t* topk, float* topw, uint32_t* blockmax,
                                uint32_t* tmask, int has_shared, const int8_t* bits, int32_t* count, int32_t* start,
                                Item* units_gu, Item* units_dn, int* n_units, int32_t* slot_token, float* slot_weight,
-                               int32_t* tok_slots, hipStream_t st);
+                               int32_t* tok_slots, const QuantX& qx, hipStream_t st);
 hipError_t launch_masks(const int32_t* topk, int T, int E, int K, int block, uint32_t* mask, hipStream_t st);
 // work units: streamed units_gu / units_dn (n_units[0] / [1], items of <= ntok slots); when `tiled` is set, the
 // chunks of the experts with more than TILED_MIN slots in tunits_gu / tunits_dn (n_units[2] / [3], Item.rb =

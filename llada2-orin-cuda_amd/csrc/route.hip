@@ -245,13 +245,24 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t k, int lane) {
 // workgroup: slots and work units for all tokens). DecodeState is zero when a call starts, and dispatch_kernel
 // leaves it zero again.
 
+// With qx.x set, the workgroup of token t first writes the A8 of x's row t (H = 2048: wave w takes columns
+// 512 w .. 512 w + 511), so routing from given logits needs no launch of its own for it.
+__device__ __forceinline__ void row_a8(const QuantX& qx, int t) {
+    if (qx.x == nullptr) return;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const size_t base = size_t(t) * 2048 + 512 * w, gi = size_t(t) * 16 + 4 * w;
+    quant_a8_512(qx.x + base, lane, qx.q + base, qx.s + gi, qx.sum + gi);
+}
+
 // grid T, 256 threads (thread = expert): logit = partials summed in chunk order; sig[t, e] = sigmoid(logit);
 // with the pool, blockmax[e] = max over tokens of the ordered key of sigmoid + bias
+template <bool QA8>
 __global__ void __launch_bounds__(256) score_kernel(const float* __restrict__ part, int nchunks,
                                                     const float* __restrict__ bias, int T, int E, int block,
                                                     int pool_on, float* __restrict__ sig,
-                                                    uint32_t* __restrict__ blockmax) {
+                                                    uint32_t* __restrict__ blockmax, QuantX qx) {
     const int t = blockIdx.x, e = threadIdx.x;
+    if constexpr (QA8) row_a8(qx, t);
     if (e >= E) return;
     float p[ROUTER_KC];
 #pragma unroll
@@ -385,16 +396,17 @@ __global__ void __launch_bounds__(256) dispatch_kernel(int T, int E, int K, cons
 // when fewer than C experts have a larger blockmax key (ties to the lower index): the four waves sort the
 // blockmax keys and each thread counts the larger ones by binary search. One token per workgroup puts T times
 // more waves on this latency-bound step than 8 tokens per workgroup.
-template <bool POOL>
+template <bool POOL, bool QA8>
 __global__ void __launch_bounds__(256) select_token_kernel(const float* __restrict__ part, int nchunks,
                                                            const float* __restrict__ sig,
                                                            const float* __restrict__ bias, int T, int E, int K,
                                                            int C, int block, float rscale, int* __restrict__ topk,
-                                                           float* __restrict__ topw, DecodeState ds) {
+                                                           float* __restrict__ topw, DecodeState ds, QuantX qx) {
     __shared__ float sig_s[MAXE];
     __shared__ uint64_t lead[4 * 8];
     __shared__ uint64_t pool_s[POOL ? MAXE : 1];
     const int t = blockIdx.x, e = threadIdx.x, lane = e & 63, w = e >> 6;
+    if constexpr (QA8) row_a8(qx, t);
     bool inpool = true;
     if constexpr (POOL) {
         const uint64_t pk =
@@ -757,16 +769,20 @@ hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, i
 
 hipError_t launch_route(const float* part, int nchunks, const float* bias, int T, int E, int K, int C, int block,
                         float rscale, float* sig, uint32_t* blockmax, int32_t* topk, float* topw, uint32_t* mask,
-                        hipStream_t st) {
+                        const QuantX& qx, hipStream_t st) {
     if (E > MAXE || block > MAXB) return hipErrorInvalidValue;
     const DecodeState ds{blockmax, mask};
     if (C < E) {
-        score_kernel<<<T, 256, 0, st>>>(part, nchunks, bias, T, E, block, 1, sig, blockmax);
-        select_token_kernel<true><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, block, rscale, topk,
-                                                      topw, ds);
+        if (qx.x) score_kernel<true><<<T, 256, 0, st>>>(part, nchunks, bias, T, E, block, 1, sig, blockmax, qx);
+        else score_kernel<false><<<T, 256, 0, st>>>(part, nchunks, bias, T, E, block, 1, sig, blockmax, qx);
+        select_token_kernel<true, false><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, block, rscale,
+                                                             topk, topw, ds, QuantX{});
+    } else if (qx.x) {
+        select_token_kernel<false, true><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, block, rscale,
+                                                             topk, topw, ds, qx);
     } else {
-        select_token_kernel<false><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, block, rscale, topk,
-                                                       topw, ds);
+        select_token_kernel<false, false><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, block, rscale,
+                                                              topk, topw, ds, qx);
     }
     return hipGetLastError();
 }
@@ -775,16 +791,20 @@ hipError_t launch_decode_route(const float* part, int nchunks, const float* bias
                                float rscale, float* sig, int32_t* topk, float* topw, uint32_t* blockmax,
                                uint32_t* tmask, int has_shared, const int8_t* bits, int32_t* count, int32_t* start,
                                Item* units_gu, Item* units_dn, int* n_units, int32_t* slot_token, float* slot_weight,
-                               int32_t* tok_slots, hipStream_t st) {
+                               int32_t* tok_slots, const QuantX& qx, hipStream_t st) {
     if (T > 32 || E > MAXE) return hipErrorInvalidValue;
     const DecodeState ds{blockmax, tmask};
     if (C < E) {
-        score_kernel<<<T, 256, 0, st>>>(part, nchunks, bias, T, E, MAXB, 1, sig, blockmax);
-        select_token_kernel<true><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, MAXB, rscale, topk, topw,
-                                                      ds);
+        if (qx.x) score_kernel<true><<<T, 256, 0, st>>>(part, nchunks, bias, T, E, MAXB, 1, sig, blockmax, qx);
+        else score_kernel<false><<<T, 256, 0, st>>>(part, nchunks, bias, T, E, MAXB, 1, sig, blockmax, qx);
+        select_token_kernel<true, false><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, MAXB, rscale, topk,
+                                                             topw, ds, QuantX{});
+    } else if (qx.x) {
+        select_token_kernel<false, true><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, MAXB, rscale, topk,
+                                                             topw, ds, qx);
     } else {
-        select_token_kernel<false><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, MAXB, rscale, topk, topw,
-                                                       ds);
+        select_token_kernel<false, false><<<T, 256, 0, st>>>(part, nchunks, sig, bias, T, E, K, C, MAXB, rscale,
+                                                              topk, topw, ds, qx);
     }
     const DispatchOut d{has_shared, 16, bits, count, start, units_gu, units_dn, n_units, slot_token, slot_weight,
                         tok_slots};
