@@ -54,8 +54,8 @@ __host__ __device__ constexpr int tiled_per(int c) {
     return c <= 0 ? 0 : (((c + tiled_chunks(c) - 1) / tiled_chunks(c)) + 15) / 16 * 16;
 }
 // Tiled work partition (per GEMM): the chunks are listed in order, chunk i spanning positions
-// [pre_i, pre_i + nrb_i c_i) with c_i the estimated cost of one of its nrb_i row-block tasks (by code width and
-// 16-slot tiles), row block r starting at pre_i + r c_i. Workgroup w of the G-workgroup grid runs the tasks whose
+// [pre_i, pre_i + s + nrb_i c_i) with s the cost of staging its activations and c_i the estimated cost of one of its
+// nrb_i row-block tasks (by code width and 16-slot tiles), row block r starting at pre_i + s + r c_i. Workgroup w of the G-workgroup grid runs the tasks whose
 // start lies in [ceil(w C / G), ceil((w + 1) C / G)), C = the total; tstart[w] = its first task as
 // chunk | rb << TASK_RB_SHIFT (tstart[G] = all chunks, rb 0).
 constexpr int TASK_RB_SHIFT = 20;
