@@ -184,16 +184,24 @@ def test_other_expert_counts(gpu, E, K, T, pool):
     G.close()
 
 
-@pytest.mark.parametrize("kind", ["zipf", "skewed"])
-def test_logits_routing(gpu, kind):
-    T = 128
-    say(f"[logits routing] {kind} T={T}")
+@pytest.mark.parametrize("kind,T,pool", [
+    ("zipf", 128, 256), ("skewed", 128, 256),
+    ("zipf", 32, 256),    # one routing block: the decode kernels
+    ("zipf", 32, 48),     # one routing block with the pool (scores first)
+    ("skewed", 200, 48),  # several blocks with the pool
+])
+def test_logits_routing(gpu, kind, T, pool):
+    """Routing from given logits; the A8 of x is written by the first per-token routing kernel."""
+    say(f"[logits routing] {kind} T={T} pool={pool}")
     L = synth.make_layer(21, mix="mixed", shared=True, zero_bias=True)
     lg = synth.logits_zipf(5, T) if kind == "zipf" else synth.logits_skewed(5, T)
-    G = make_gpu_layer(L, 256)
+    G = make_gpu_layer(L, pool)
     x = synth.make_x(77, T)
     out = run_layer(G, x, gpu, logits=lg)
-    r = oracle.Layer(L).forward(x, logits=lg, C=256)
+    r = oracle.Layer(L).forward(x, logits=lg, C=pool)
+    assert np.array_equal(G.read("xq", (T, 2048), np.int8), r["xq"]), "A8 codes of x differ"
+    assert np.array_equal(G.read("xs", (T, 16), np.float32).view(np.uint32), r["xs"].view(np.uint32))
+    assert np.array_equal(G.read("xsum", (T, 16), np.int32), r["xsum"])
     check_full(G, r, T, 8, True)
     assert np.array_equal(out.view(np.uint32), r["out"].view(np.uint32))
     G.close()
