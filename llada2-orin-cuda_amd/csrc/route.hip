@@ -9,6 +9,8 @@ namespace {
 
 constexpr int MAXB = 32;    // tokens per routing block (one 32-bit token mask per expert)
 constexpr int MAXE = 256;   // experts (one thread each)
+constexpr int PLAN_NT = 1024;          // planner threads: 4 per expert
+constexpr int MAXB_BLOCKS = 128;       // routing blocks whose masks the planner holds in registers (32 per thread)
 
 // logits partial c: fma chain over k = c H/8 .. (c+1) H/8 - 1 ascending from 0 (the summation order is fixed so
 // the CPU checker reproduces it). Workgroup tile: TT tokens x EW experts of one K chunk, the chunk's x slice and
@@ -489,16 +491,18 @@ __global__ void __launch_bounds__(256) masks_kernel(const int* __restrict__ topk
 // an expert block-major then token-ascending. An expert with more than TILED_MIN slots (when `tiled`) gets tiled
 // units (chunks of <= TILED_NTOK slots x tiled row blocks), otherwise streamed units (items of <= ntok slots x
 // streamed row blocks). Both lists are ordered heaviest first (shared expert, then 8 / 4 / 3 / 2-bit experts).
-// One workgroup, thread = expert.
-__global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ mask, int T, int E, int K, int block,
-                                                   int has_shared, int ntok, int tiled,
-                                                   const int8_t* __restrict__ bits, int* __restrict__ count,
-                                                   int* __restrict__ start, int* __restrict__ bpre,
-                                                   Item* __restrict__ units_gu, Item* __restrict__ units_dn,
-                                                   Item* __restrict__ tunits_gu, Item* __restrict__ tunits_dn,
-                                                   int* __restrict__ n_units, int g_gu, int g_dn,
-                                                   int* __restrict__ tstart, int max_chunks) {
-    constexpr int NBR = 64;                    // token masks of the first NBR blocks stay in registers
+// One workgroup of four threads per expert: the block masks are split in four contiguous ranges.
+__global__ void __launch_bounds__(PLAN_NT) plan_kernel(const uint32_t* __restrict__ mask, int T, int E, int K,
+                                                       int block, int has_shared, int ntok, int tiled,
+                                                       const int8_t* __restrict__ bits, int* __restrict__ count,
+                                                       int* __restrict__ start, int* __restrict__ bpre,
+                                                       Item* __restrict__ units_gu, Item* __restrict__ units_dn,
+                                                       Item* __restrict__ tunits_gu, Item* __restrict__ tunits_dn,
+                                                       int* __restrict__ n_units, int g_gu, int g_dn,
+                                                       int* __restrict__ tstart, int max_chunks) {
+    constexpr int NP = PLAN_NT / MAXE;         // threads per expert: each takes a contiguous range of blocks
+    constexpr int NBR = MAXB_BLOCKS / NP;      // block masks of a range held in registers
+    constexpr int NWAVE = PLAN_NT / 64;
     // chunk tables (max_chunks entries): row-block tasks of both GEMMs, then their positions [n_chunks + 1]
     extern __shared__ uint32_t plan_lds[];
     uint32_t* task_gu = plan_lds;
@@ -506,38 +510,51 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     int* pre_gu = reinterpret_cast<int*>(task_dn + max_chunks);
     int* pre_dn = pre_gu + max_chunks + 1;
     int* owner = pre_dn + max_chunks + 1;      // expert of each chunk
-    __shared__ int wt_i[4], wt_c[4];
+    __shared__ int wt_i[NWAVE], wt_c[NWAVE];
     __shared__ uint64_t wt[4][4];
     __shared__ uint64_t tot[4];
     __shared__ int first_l[MAXE + 1], cnt_l[MAXE + 1], st_l[MAXE + 1], bits_l[MAXE + 1];
-    const int e = threadIdx.x, nb = (T + block - 1) / block, lane = e & 63, w = e >> 6;
+    __shared__ int cpart_s[NP][MAXE];          // tokens of expert e in part p's block range
+    const int tid = threadIdx.x, e = tid % MAXE, part = tid / MAXE, nb = (T + block - 1) / block;
+    const int lane = tid & 63, wv = tid >> 6, w = wv & 3;   // (w: the wave within the expert-scan group)
+    const bool g0 = part == 0;                 // the expert's lead thread (scans, units)
     PLAN_TRACE(0);
-    // token masks: unconditional loads at clamped indices, so that each batch is issued back to back
-    const int ec = min(e, E - 1);
+    // token masks of the part's block range [b_lo, b_hi): unconditional loads at clamped indices, so that the
+    // batch is issued back to back
+    const int ec = min(e, E - 1), nbp = (nb + NP - 1) / NP, b_lo = min(nb, part * nbp), b_hi = min(nb, b_lo + nbp);
     // code widths read up front, with the masks: a load after them would expose its own latency
     const int bw_ld = bits[ec], sbits_ld = has_shared ? bits[E] : 8;
     uint32_t mv[NBR];
 #pragma unroll
-    for (int j = 0; j < NBR; ++j) mv[j] = mask[size_t(min(j, nb - 1)) * E + ec];
-    int c = 0;
+    for (int j = 0; j < NBR; ++j) mv[j] = mask[size_t(min(b_lo + j, nb - 1)) * E + ec];
+    int cp = 0;
 #pragma unroll
-    for (int j = 0; j < NBR; ++j) c += j < nb ? __popc(mv[j]) : 0;
-    for (int b0 = NBR; b0 < nb; b0 += 16) {
+    for (int j = 0; j < NBR; ++j) cp += b_lo + j < b_hi ? __popc(mv[j]) : 0;
+    for (int b0 = b_lo + NBR; b0 < b_hi; b0 += 16) {   // ranges longer than the registers hold
         uint32_t m2[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) m2[j] = mask[size_t(min(b0 + j, nb - 1)) * E + ec];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) c += b0 + j < nb ? __popc(m2[j]) : 0;
+        for (int j = 0; j < 16; ++j) cp += b0 + j < b_hi ? __popc(m2[j]) : 0;
     }
-    if (e >= E) c = 0;
+    if (e >= E) cp = 0;
+    cpart_s[part][e] = cp;
+    __syncthreads();
+    int c = 0, cbefore = 0;   // the expert's slots; those in the blocks before the part's range
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+        const int v = cpart_s[pp][e];
+        cbefore += pp < part ? v : 0;
+        c += v;
+    }
     PLAN_TRACE(1);
     const bool big = e < E && tiled && c > 0;
     const bool sbig = has_shared && tiled;
     const int nsch = sbig ? tiled_chunks(T) : 0;
     const int bw = e < E ? bw_ld : 2, cls = width_class(bw);
     const int nit = e < E && !big ? (c + ntok - 1) / ntok : 0, nch = big ? tiled_chunks(c) : 0;
-    // one pass of inclusive scans over the experts: slots, tiled chunks, and per width class (16-bit fields) the
-    // streamed units of both lists and the tiled chunks
+    // one pass of inclusive scans over the experts (lead threads): slots, tiled chunks, and per width class
+    // (16-bit fields) the streamed units of both lists and the tiled chunks
     int incl = c;
     uint64_t s0 = uint64_t(nit * gemm_row_blocks(false, bw)) << (16 * cls);
     uint64_t s1 = uint64_t(nit * gemm_row_blocks(true, bw)) << (16 * cls);
@@ -547,7 +564,7 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     s0 = wave_incl_scan(s0);
     s1 = wave_incl_scan(s1);
     t0 = wave_incl_scan(t0);
-    if (lane == 63) {
+    if (g0 && lane == 63) {
         wt_i[w] = incl;
         wt[w][0] = s0;
         wt[w][1] = s1;
@@ -560,7 +577,7 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
         s1 += wt[i][1];
         t0 += wt[i][2];
     }
-    if (e == 255) {
+    if (tid == MAXE - 1) {
         tot[0] = s0;
         tot[1] = s1;
         tot[2] = t0;
@@ -581,28 +598,32 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
         bd += int((tot[1] >> (16 * k)) & 0xFFFFu);
         bt += int((tot[2] >> (16 * k)) & 0xFFFFu);
     }
+    // (the scans above ran in every part on identical values; only part 0's results are used below)
     const int st = incl - c;
     if (e < E) {
-        count[e] = c;
-        start[e] = st;
-        int run = st;
+        // slot base of each (block, expert) of the part's range
+        int run = st + cbefore;
 #pragma unroll
         for (int j = 0; j < NBR; ++j)
-            if (j < nb) {
-                bpre[size_t(j) * E + e] = run;
+            if (b_lo + j < b_hi) {
+                bpre[size_t(b_lo + j) * E + e] = run;
                 run += __popc(mv[j]);
             }
-        for (int b0 = NBR; b0 < nb; b0 += 16) {
+        for (int b0 = b_lo + NBR; b0 < b_hi; b0 += 16) {
             uint32_t m2[16];
 #pragma unroll
             for (int j = 0; j < 16; ++j) m2[j] = mask[size_t(min(b0 + j, nb - 1)) * E + e];
 #pragma unroll
             for (int j = 0; j < 16; ++j)
-                if (b0 + j < nb) {
+                if (b0 + j < b_hi) {
                     bpre[size_t(b0 + j) * E + e] = run;
                     run += __popc(m2[j]);
                 }
         }
+    }
+    if (g0 && e < E) {
+        count[e] = c;
+        start[e] = st;
         if (big) {   // the chunks are written below, one thread per chunk
             first_l[e] = ot;
             cnt_l[e] = c;
@@ -615,15 +636,15 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     }
     if (ns) emit_shared_units(E, T, K, ntok, sbits, units_gu, units_dn);
     if (sbig) {
-        if (e == 0) {
+        if (tid == 0) {
             first_l[E] = 0;
             cnt_l[E] = T;
             st_l[E] = T * K;
             bits_l[E] = sbits;
         }
-        for (int j = e; j < nsch; j += blockDim.x) owner[j] = E;
+        for (int j = tid; j < nsch; j += blockDim.x) owner[j] = E;
     }
-    if (e == 0) {
+    if (tid == 0) {
         n_units[0] = bg;
         n_units[1] = bd;
         n_units[2] = bt;
@@ -634,7 +655,7 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     // the tiled chunks: tiled_per(c) slots of an expert's c each, the last one shorter (Item.rb unused)
     __syncthreads();
     const int n = bt;
-    for (int j = e; j < n; j += blockDim.x) {
+    for (int j = tid; j < n; j += blockDim.x) {
         const int x = owner[j], cx = cnt_l[x], pc = tiled_per(cx), jj = j - first_l[x];
         const Item it{x, st_l[x] + jj * pc, min(pc, cx - jj * pc), 0};
         tunits_gu[j] = it;
@@ -643,7 +664,7 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     }
     // chunk positions of both GEMMs: scans of the chunk costs (each thread a run of consecutive chunks)
     __syncthreads();
-    const int per = (n + blockDim.x - 1) / blockDim.x, j0 = min(n, e * per), j1 = min(n, j0 + per);
+    const int per = (n + blockDim.x - 1) / blockDim.x, j0 = min(n, tid * per), j1 = min(n, j0 + per);
     auto cost = [](uint32_t t, int stage) { return stage + int(t >> 8) * int(t & 255u); };
     int run0 = 0, run1 = 0;
     for (int j = j0; j < j1; ++j) {
@@ -654,11 +675,11 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
     inc0 = wave_incl_scan(inc0);
     inc1 = wave_incl_scan(inc1);
     if (lane == 63) {
-        wt_i[w] = inc0;
-        wt_c[w] = inc1;
+        wt_i[wv] = inc0;
+        wt_c[wv] = inc1;
     }
     __syncthreads();
-    for (int i = 0; i < w; ++i) {
+    for (int i = 0; i < wv; ++i) {
         inc0 += wt_i[i];
         inc1 += wt_c[i];
     }
@@ -670,7 +691,7 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
         run0 += cost(task_gu[j], STAGE_COST_GU);
         run1 += cost(task_dn[j], STAGE_COST_DN);
     }
-    if (e == blockDim.x - 1) {
+    if (tid == int(blockDim.x) - 1) {
         pre_gu[n] = inc0;
         pre_dn[n] = inc1;
     }
@@ -686,8 +707,8 @@ __global__ void __launch_bounds__(256) plan_kernel(const uint32_t* __restrict__ 
         const uint32_t* task = m ? task_dn : task_gu;
         int* ts = tstart + (m ? g_gu + 1 : 0);
         const long long C = P[n];
-        if (e == 0) ts[G] = n;
-        for (int q = e; q < G; q += blockDim.x) {
+        if (tid == 0) ts[G] = n;
+        for (int q = tid; q < G; q += blockDim.x) {
             const long long lo = C == 0 ? 0 : floor_div((long long)q * C + G - 1, G);
             if (lo >= C) {
                 ts[q] = n;
@@ -830,7 +851,7 @@ hipError_t launch_plan(const uint32_t* mask, int T, int E, int K, int block, int
                        Item* units_dn, Item* tunits_gu, Item* tunits_dn, int* n_units, int g_gu, int g_dn,
                        int* tstart, int max_chunks, hipStream_t st) {
     const size_t lds = (5 * size_t(max_chunks) + 2) * sizeof(uint32_t);
-    plan_kernel<<<1, 256, lds, st>>>(mask, T, E, K, block, has_shared, ntok, tiled, bits, count, start, bpre,
+    plan_kernel<<<1, PLAN_NT, lds, st>>>(mask, T, E, K, block, has_shared, ntok, tiled, bits, count, start, bpre,
                                      units_gu, units_dn, tunits_gu, tunits_dn, n_units, g_gu, g_dn, tstart,
                                      max_chunks);
     return hipGetLastError();

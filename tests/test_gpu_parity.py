@@ -235,6 +235,7 @@ def test_tiled_units_bit_exact(gpu, T, mix, kind):
     (2048, "mixed", True, 256, "zipf"),   # one layer of config 3
     (4096, 2, False, 256, "uniform"),     # config 4, 2-bit
     (4096, 8, False, 256, "skewed"),      # config 4, 8-bit, 16 experts take half the slots
+    (5120, 4, False, 256, "uniform"),     # 160 routing blocks: more block masks than the planner holds in registers
 ])
 def test_full_size_batch_invariance(gpu, T, mix, shared, pool, kind):
     """At the configs' full token counts the GPU layer runs every expert through the work lists and chunking of
