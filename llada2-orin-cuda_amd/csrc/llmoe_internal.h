@@ -249,11 +249,11 @@ __device__ __forceinline__ void fwht512_a8(const uint16_t* __restrict__ zrow, in
 // A8 of 512 consecutive values by one wave (engine/ops.cu:42-66): lane l owns values 8l .. 8l+7, a 128-group is
 // 16 lanes; s = max(max|v| / 127, 1e-30), q = clamp(rint(v / s), +-127). Writes the lane's 8 codes and, from the
 // group's first lane, its scale and code sum (s4 / sum4: the 4 groups of the 512). All 64 lanes must be active.
-__device__ __forceinline__ void quant_a8_512(const float* __restrict__ x, int lane, int8_t* __restrict__ q,
-                                             float* __restrict__ s4, int* __restrict__ sum4) {
-    const float4 a = *reinterpret_cast<const float4*>(x + 8 * lane);
-    const float4 b = *reinterpret_cast<const float4*>(x + 8 * lane + 4);
-    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+// A8 of 8 values per lane, 16 lanes per 128-group (lanes 16g .. 16g+15 hold group g's values in order): the
+// lane's 8 codes go to q8, and lane 16g writes its group's scale and code sum to *s and *sum (nothing is written
+// when store is false).
+__device__ __forceinline__ void quant_a8_8(const float (&v)[8], int lane, int8_t* __restrict__ q8,
+                                           float* __restrict__ s, int* __restrict__ sum, bool store = true) {
     float m = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
@@ -268,12 +268,19 @@ __device__ __forceinline__ void quant_a8_512(const float* __restrict__ x, int la
         if (j < 4) w0 |= uint32_t(qq & 0xFF) << (8 * j);
         else w1 |= uint32_t(qq & 0xFF) << (8 * (j - 4));
     }
-    *reinterpret_cast<uint2*>(q + 8 * lane) = make_uint2(w0, w1);
+    if (store) *reinterpret_cast<uint2*>(q8) = make_uint2(w0, w1);
     tot = group16_sum(tot);
-    if ((lane & 15) == 0) {
-        s4[lane >> 4] = sc;
-        sum4[lane >> 4] = tot;
+    if (store && (lane & 15) == 0) {
+        *s = sc;
+        *sum = tot;
     }
+}
+__device__ __forceinline__ void quant_a8_512(const float* __restrict__ x, int lane, int8_t* __restrict__ q,
+                                             float* __restrict__ s4, int* __restrict__ sum4) {
+    const float4 a = *reinterpret_cast<const float4*>(x + 8 * lane);
+    const float4 b = *reinterpret_cast<const float4*>(x + 8 * lane + 4);
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    quant_a8_8(v, lane, q + 8 * lane, s4 + (lane >> 4), sum4 + (lane >> 4));
 }
 
 // the A8 of the layer input (H = 2048) done by the first per-token routing kernel when routing from given logits

@@ -16,8 +16,8 @@ constexpr int MAXB_BLOCKS = 128;       // routing blocks whose masks the planner
 // the CPU checker reproduces it). Workgroup tile: TT tokens x EW experts of one K chunk, the chunk's x slice and
 // its Wr slice (transposed, k contiguous per expert) staged in LDS by one batch of loads; each thread runs one
 // chain per (token, expert) it owns. grid (E/EW, ceil(T/TT), 8).
-// With q != nullptr the workgroups of expert slice 0 also write the A8 of their x slice (two 128-groups per
-// token, the same operations as quant_a8_kernel), so the layer input is quantised without a launch of its own.
+// With q != nullptr the workgroups also write the A8 of the x slice (two 128-groups per token, the same operations
+// as quant_a8_kernel, spread over the expert slices), so the layer input is quantised without a launch of its own.
 __device__ __forceinline__ uint32_t okey(float v) {        // order-preserving unsigned image of a float
     const uint32_t u = __float_as_uint(v);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -101,37 +101,20 @@ __global__ void __launch_bounds__(NT) router_logits_kernel(const float* __restri
 #pragma unroll
             for (int j = 0; j < EPT; ++j) part[(size_t(c) * T + t) * E + e0 + j * EG + eg] = acc[i][j];
     }
-    if (q != nullptr && blockIdx.x == 0 && tid < TT * 8) {
-        // A8 of the slice: (token, group) pair p = tid / 4, 4 threads x 32 values each
-        const int p = tid >> 2, part4 = tid & 3, tt = p >> 1, gl = p & 1;
-        const float* v = xs + tt * RXS + gl * GROUP + part4 * 32;
-        float m = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) m = fmaxf(m, fabsf(v[j]));
-        m = fmaxf(m, xor_lane(m, 1));
-        m = fmaxf(m, xor_lane(m, 2));
-        const float sc = fmaxf(m / 127.0f, 1e-30f);
-        int tot = 0;
-        uint32_t w[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) w[j] = 0u;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            const int qq = int(fminf(fmaxf(__builtin_rintf(v[j] / sc), -127.0f), 127.0f));
-            tot += qq;
-            w[j >> 2] |= uint32_t(qq & 0xFF) << (8 * (j & 3));
-        }
-        tot += xor_lane(tot, 1);
-        tot += xor_lane(tot, 2);
-        if (t0 + tt < T) {
-            int8_t* dst = q + size_t(t0 + tt) * H + kb + gl * GROUP + part4 * 32;
-            *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
-            *reinterpret_cast<uint4*>(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
-            if (part4 == 0) {
-                const size_t gi = size_t(t0 + tt) * (H / GROUP) + c * (RKW / GROUP) + gl;
-                qs[gi] = sc;
-                qsum[gi] = tot;
-            }
+    if (q != nullptr) {
+        // A8 of the chunk's x slice (two 128-groups per token), one pair of tokens per wave: lanes 0-31 the first
+        // token, 32-63 the second, 8 values each; wave w of expert slice b takes job w E/EW + b, so the jobs fall
+        // on different workgroups and no workgroup adds more than one job to its logits
+        constexpr int NWV = NT / 64;
+        const int lane = tid & 63;
+        for (int j = (tid >> 6) * int(gridDim.x) + int(blockIdx.x); j < TT / 2; j += NWV * int(gridDim.x)) {
+            const int tt = 2 * j + (lane >> 5), l = lane & 31;
+            const float4 a = *reinterpret_cast<const float4*>(xs + tt * RXS + 8 * l);
+            const float4 b = *reinterpret_cast<const float4*>(xs + tt * RXS + 8 * l + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            const int t = t0 + tt;   // (rows beyond T: computed on zeros, not written)
+            const size_t gi = size_t(t) * (H / GROUP) + c * (RKW / GROUP) + (l >> 4);
+            quant_a8_8(v, lane, q + size_t(t) * H + kb + 8 * l, qs + gi, qsum + gi, t < T);
         }
     }
 }
