@@ -291,6 +291,10 @@ __global__ void __launch_bounds__(256) dispatch_kernel(int T, int E, int K, cons
     __shared__ uint64_t tot_g, tot_d;
     const int e = threadIdx.x;
     const uint32_t m = e < E ? ds.tmask[e] : 0u;
+    // the (token, k) pairs of the placement below (T K <= 256: at most one per thread), read up front so that
+    // their latency overlaps the scans
+    const int ex0 = e < T * K ? topk[e] : 0;
+    const float w0 = e < T * K ? topw[e] : 0.0f;
     if (e < E) {
         m_s[e] = m;
         ds.tmask[e] = 0u;
@@ -362,8 +366,8 @@ __global__ void __launch_bounds__(256) dispatch_kernel(int T, int E, int K, cons
     // place every (token, k) pair
     for (int p = e; p < T * K; p += 256) {
         const int t = p / K;
-        const int ex = topk[p];
-        const float w = topw[p];
+        const int ex = p == e ? ex0 : topk[p];
+        const float w = p == e ? w0 : topw[p];
         const int sl = start_s[ex] + __popc(m_s[ex] & ((1u << t) - 1u));
         d.slot_token[sl] = t;
         d.slot_weight[sl] = w;
