@@ -102,7 +102,7 @@ int llmoe_dense_create(int rows, int k, int bits, const uint8_t* blob, size_t bl
                                         size_t(tiled_chunks(max_tokens)));
     bool ok = D->G > 0 && alloc(reinterpret_cast<void**>(&D->arena), bytes) &&
               alloc(reinterpret_cast<void**>(&D->off), sizeof(uint64_t)) &&
-              alloc(reinterpret_cast<void**>(&D->bits_d), 1) &&
+              alloc(reinterpret_cast<void**>(&D->bits_d), 4) &&   // a whole dword: read by scalar dword loads
               alloc(reinterpret_cast<void**>(&D->units), cap * sizeof(Item)) &&
               alloc(reinterpret_cast<void**>(&D->n_units), sizeof(int)) &&
               alloc(reinterpret_cast<void**>(&D->tstart), size_t(D->G + 1) * sizeof(int));

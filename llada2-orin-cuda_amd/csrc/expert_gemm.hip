@@ -134,7 +134,8 @@ __host__ __device__ constexpr int lds_bytes() {
 }
 
 template <int BITS, int MODE, int NT>
-__device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uint8_t* lds, int row_block) {
+__device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, const uint8_t* mat_e, uint8_t* lds,
+                                          int row_block) {
     constexpr int NSB = Geo<MODE>::NSB, SPW = Geo<MODE>::template spw<BITS>(), NSTEP = NSB * SPW;
     constexpr int D = Ring<BITS>::D < NSTEP ? Ring<BITS>::D : NSTEP;
     static_assert(NSTEP % 4 == 0 && 4 % D == 0, "ring geometry");
@@ -144,7 +145,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, col = lane & 15;
     if ((row_block + 1) * WAVES * SPW * 16 > a.R) return;    // not a row block of this code width
     const int strip0 = (row_block * WAVES + wave) * SPW;
-    const uint8_t* mat = a.base + a.off[it.expert] + size_t(strip0) * NSB * SBB;
+    const uint8_t* mat = mat_e + size_t(strip0) * NSB * SBB;
 
     // weight prefetch first: its latency overlaps the meta and B staging below
     Step<BITS> ring[D];
@@ -399,17 +400,31 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, uin
 // Measured at 32 tokens and not kept: units claimed from a device counter as workgroups become free (0.0625 ->
 // 0.073 ms per step: same-address device-scope atomics serialise across the 8 XCDs), and a second round assigned
 // in reverse (0.0610 -> 0.0631 ms).
+// a pointer into memory this kernel does not write, as a constant-address-space pointer (scalar loads)
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(4))) T* const_ptr(const T* p) {
+    return (const __attribute__((address_space(4))) T*)(p);
+}
+
 template <int MODE, int NT>
 __global__ void __launch_bounds__(WAVES * 64, NT == 1 ? 3 : 1) expert_gemm(GemmArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
+    // the unit and the expert's code width and matrix offset are read through the scalar cache (constant address
+    // space: the lists are written by earlier kernels only), the width and offset together, so the weight stream
+    // starts after two short dependent loads
     const int n = *a.n_items;
     for (int u = blockIdx.x; u < n; u += gridDim.x) {
-        const Item it = a.items[u];
-        const int bits = a.bits[it.expert];
-        if (bits == 2) gemm_body<2, MODE, NT>(a, it, lds, it.rb);
-        else if (bits == 3) gemm_body<3, MODE, NT>(a, it, lds, it.rb);
-        else if (bits == 4) gemm_body<4, MODE, NT>(a, it, lds, it.rb);
-        else gemm_body<8, MODE, NT>(a, it, lds, it.rb);
+        const auto* ip = const_ptr(reinterpret_cast<const int*>(a.items + u));
+        const Item it{ip[0], ip[1], ip[2], ip[3]};
+        const uint64_t off = *const_ptr(a.off + it.expert);
+        const uint32_t bw4 = *const_ptr(reinterpret_cast<const uint32_t*>(a.bits) + (it.expert >> 2));
+        asm volatile("" ::"s"(off), "s"(bw4));   // both loads in flight together, before the branch on the width
+        const int bits = int(bw4 >> (8 * (it.expert & 3))) << 24 >> 24;
+        const uint8_t* mat_e = a.base + off;
+        if (bits == 2) gemm_body<2, MODE, NT>(a, it, mat_e, lds, it.rb);
+        else if (bits == 3) gemm_body<3, MODE, NT>(a, it, mat_e, lds, it.rb);
+        else if (bits == 4) gemm_body<4, MODE, NT>(a, it, mat_e, lds, it.rb);
+        else gemm_body<8, MODE, NT>(a, it, mat_e, lds, it.rb);
         __syncthreads();   // the next unit re-stages the LDS
     }
 }
