@@ -400,12 +400,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, con
 // Measured at 32 tokens and not kept: units claimed from a device counter as workgroups become free (0.0625 ->
 // 0.073 ms per step: same-address device-scope atomics serialise across the 8 XCDs), and a second round assigned
 // in reverse (0.0610 -> 0.0631 ms).
-// a pointer into memory this kernel does not write, as a constant-address-space pointer (scalar loads)
-template <class T>
-__device__ __forceinline__ const __attribute__((address_space(4))) T* const_ptr(const T* p) {
-    return (const __attribute__((address_space(4))) T*)(p);
-}
-
 template <int MODE, int NT>
 __global__ void __launch_bounds__(WAVES * 64, NT == 1 ? 3 : 1) expert_gemm(GemmArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];

@@ -182,6 +182,12 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
 }
 
+// A pointer into memory this kernel does not write, as a constant-address-space pointer (scalar loads)
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(4))) T* const_ptr(const T* p) {
+    return (const __attribute__((address_space(4))) T*)(p);
+}
+
 __device__ __forceinline__ float group16_max(float m) {
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, xor_lane(m, o));

@@ -445,11 +445,10 @@ __device__ __forceinline__ void trace_put(int slot, unsigned long long v) {
 #endif
 
 template <int BITS, int MODE, int NTILE>
-__device__ __forceinline__ void tiled_body(const GemmArgs& a, const Item& it, uint8_t* lds, int rb0, int rb1, int u) {
+__device__ __forceinline__ void tiled_body(const GemmArgs& a, const Item& it, const uint8_t* mat, uint8_t* lds,
+                                           int rb0, int rb1, int u) {
     constexpr int K = MODE == GEMM_DOWN ? 512 : 2048;
     (void)u;
-    // the expert's matrix (one load per unit, not one per row block; the compiler keeps it wave-uniform)
-    const uint8_t* mat = a.base + a.off[it.expert];
     // row block rb + 1's first weights are requested between rb's products and rb's stores: the weight loads then
     // precede the output stores in the in-order memory counter, so waiting for them never waits for the stores
     RowRegs<BITS, MODE> r;
@@ -479,12 +478,19 @@ __global__ void __launch_bounds__(nthreads_for(MODE == GEMM_DOWN ? 512 : 2048)) 
     // hot expert -- listed one after another -- share that XCD's L2 for the expert's weights
     const int G = gridDim.x;
     const int p = G % NXCD ? int(blockIdx.x) : int(blockIdx.x % NXCD) * (G / NXCD) + int(blockIdx.x / NXCD);
-    const int s0 = a.tstart[p], s1 = a.tstart[p + 1];
+    const int s0 = *const_ptr(a.tstart + p), s1 = *const_ptr(a.tstart + p + 1);
     const int c0 = s0 & CMASK, r0 = s0 >> TASK_RB_SHIFT, c1 = s1 & CMASK, r1 = s1 >> TASK_RB_SHIFT;
     int u = p * 16;   // trace slot (timing builds)
     for (int c = c0; c < c1 || (c == c1 && r1 > 0); ++c) {
-        const Item it = a.items[c];
-        const int bits = a.bits[it.expert];
+        // the chunk, and the expert's matrix offset and code width together, by scalar loads (the lists are
+        // written by earlier kernels only)
+        const auto* ip = const_ptr(reinterpret_cast<const int*>(a.items + c));
+        const Item it{ip[0], ip[1], ip[2], ip[3]};
+        const uint64_t off = *const_ptr(a.off + it.expert);
+        const uint32_t bw4 = *const_ptr(reinterpret_cast<const uint32_t*>(a.bits) + (it.expert >> 2));
+        asm volatile("" ::"s"(off), "s"(bw4));
+        const int bits = int(bw4 >> (8 * (it.expert & 3))) << 24 >> 24;
+        const uint8_t* mat = a.base + off;
         const int nrb = MODE == GEMM_DENSE ? a.R / (16 * tiled_waves(false) * tiled_spw(false, bits))
                                            : tiled_row_blocks(MODE == GEMM_DOWN, bits);
         const int rb0 = c == c0 ? r0 : 0, rb1 = c == c1 ? r1 : nrb;
@@ -497,25 +503,25 @@ __global__ void __launch_bounds__(nthreads_for(MODE == GEMM_DOWN ? 512 : 2048)) 
         // token tiles actually present (a chunk has <= 64 slots; absent tiles are not computed)
         const int nt = (it.ntok + 15) >> 4;
         if (nt > 3) {
-            if (bits == 2) tiled_body<2, MODE, 4>(a, it, lds, rb0, rb1, u);
-            else if (bits == 3) tiled_body<3, MODE, 4>(a, it, lds, rb0, rb1, u);
-            else if (bits == 4) tiled_body<4, MODE, 4>(a, it, lds, rb0, rb1, u);
-            else tiled_body<8, MODE, 4>(a, it, lds, rb0, rb1, u);
+            if (bits == 2) tiled_body<2, MODE, 4>(a, it, mat, lds, rb0, rb1, u);
+            else if (bits == 3) tiled_body<3, MODE, 4>(a, it, mat, lds, rb0, rb1, u);
+            else if (bits == 4) tiled_body<4, MODE, 4>(a, it, mat, lds, rb0, rb1, u);
+            else tiled_body<8, MODE, 4>(a, it, mat, lds, rb0, rb1, u);
         } else if (nt == 3) {
-            if (bits == 2) tiled_body<2, MODE, 3>(a, it, lds, rb0, rb1, u);
-            else if (bits == 3) tiled_body<3, MODE, 3>(a, it, lds, rb0, rb1, u);
-            else if (bits == 4) tiled_body<4, MODE, 3>(a, it, lds, rb0, rb1, u);
-            else tiled_body<8, MODE, 3>(a, it, lds, rb0, rb1, u);
+            if (bits == 2) tiled_body<2, MODE, 3>(a, it, mat, lds, rb0, rb1, u);
+            else if (bits == 3) tiled_body<3, MODE, 3>(a, it, mat, lds, rb0, rb1, u);
+            else if (bits == 4) tiled_body<4, MODE, 3>(a, it, mat, lds, rb0, rb1, u);
+            else tiled_body<8, MODE, 3>(a, it, mat, lds, rb0, rb1, u);
         } else if (nt == 2) {
-            if (bits == 2) tiled_body<2, MODE, 2>(a, it, lds, rb0, rb1, u);
-            else if (bits == 3) tiled_body<3, MODE, 2>(a, it, lds, rb0, rb1, u);
-            else if (bits == 4) tiled_body<4, MODE, 2>(a, it, lds, rb0, rb1, u);
-            else tiled_body<8, MODE, 2>(a, it, lds, rb0, rb1, u);
+            if (bits == 2) tiled_body<2, MODE, 2>(a, it, mat, lds, rb0, rb1, u);
+            else if (bits == 3) tiled_body<3, MODE, 2>(a, it, mat, lds, rb0, rb1, u);
+            else if (bits == 4) tiled_body<4, MODE, 2>(a, it, mat, lds, rb0, rb1, u);
+            else tiled_body<8, MODE, 2>(a, it, mat, lds, rb0, rb1, u);
         } else {
-            if (bits == 2) tiled_body<2, MODE, 1>(a, it, lds, rb0, rb1, u);
-            else if (bits == 3) tiled_body<3, MODE, 1>(a, it, lds, rb0, rb1, u);
-            else if (bits == 4) tiled_body<4, MODE, 1>(a, it, lds, rb0, rb1, u);
-            else tiled_body<8, MODE, 1>(a, it, lds, rb0, rb1, u);
+            if (bits == 2) tiled_body<2, MODE, 1>(a, it, mat, lds, rb0, rb1, u);
+            else if (bits == 3) tiled_body<3, MODE, 1>(a, it, mat, lds, rb0, rb1, u);
+            else if (bits == 4) tiled_body<4, MODE, 1>(a, it, mat, lds, rb0, rb1, u);
+            else tiled_body<8, MODE, 1>(a, it, mat, lds, rb0, rb1, u);
         }
         __syncthreads();   // the next chunk re-stages the activations
         TRACE_AT(u, 2);
