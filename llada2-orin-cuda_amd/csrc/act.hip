@@ -46,9 +46,9 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
     const int t = blockIdx.x;
     // columns [h0, h1) of the row: gridDim.y slices, so that a small T still spreads over many CUs
     const int hw = H / int(gridDim.y), h0 = int(blockIdx.y) * hw, h1 = h0 + hw;
-    int sl[MAX_KK];
+    int sl[MAX_KK];   // (scalar loads: the row's slots are the same for the whole workgroup)
 #pragma unroll
-    for (int k = 0; k < MAX_KK; ++k) sl[k] = k < kk ? tok_slots[t * K1 + k] : 0;
+    for (int k = 0; k < MAX_KK; ++k) sl[k] = k < kk ? *const_ptr(tok_slots + t * K1 + k) : 0;
     // R float4 columns per thread per pass: every load of the pass is in flight before the ordered sums
     constexpr int R = 2;
     for (int hb = h0 + threadIdx.x * 4; hb < h1; hb += blockDim.x * 4 * R) {
@@ -134,7 +134,7 @@ __global__ void __launch_bounds__(256) combine_norm_kernel(const float* __restri
     const int t = blockIdx.x, i = threadIdx.x, lane = i & 63;
     int sl[MAX_KK];
 #pragma unroll
-    for (int k = 0; k < MAX_KK; ++k) sl[k] = k < kk ? tok_slots[t * K1 + k] : 0;
+    for (int k = 0; k < MAX_KK; ++k) sl[k] = k < kk ? *const_ptr(tok_slots + t * K1 + k) : 0;
     float4 ya[MAX_KK], yb[MAX_KK];
 #pragma unroll
     for (int k = 0; k < MAX_KK; ++k)
