@@ -443,7 +443,6 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     // gate_up: B rows are token rows of x'
     g.items = L->units_gu;
     g.n_items = L->n_units;
-    g.items_cap = int(L->items_cap * MAX_UNITS_PER_ITEM);
     g.off = L->gu_off_d;
     g.slot_token = L->slot_token;
     g.xq = xq; g.xs = xs; g.xsum = xsum;

@@ -305,7 +305,6 @@ struct GemmArgs {
     const int8_t* bits;         // [E+1]
     const Item* items;          // work units
     const int* n_items;         // device count of work units (the persistent grid loops over them)
-    int items_cap;              // streamed: entries of `items` (read ahead of the count when > 0)
     const int* slot_token;      // gate_up: B row of slot s is token slot_token[s]; nullptr: row = slot
     const int8_t* xq;           // B rows, int8 [rows, K]
     const float* xs;            // [rows, K/128]
