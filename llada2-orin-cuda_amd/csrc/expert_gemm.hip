@@ -142,7 +142,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, con
     constexpr int K = NSB * SB_K, G = K / GROUP, NTOK = 16 * NT, LDQ = K + 16;
     constexpr size_t SBB = sb_bytes(BITS);
     constexpr int ZOFF = BITS == 8 ? 128 : 0;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, col = lane & 15;
+    // (the thread index made opaque: values derived from it are recomputed per unit, not kept live -- and
+    // spilled -- across the unit loop)
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63, wave = tid >> 6, q = lane >> 4, col = lane & 15;
     if ((row_block + 1) * WAVES * SPW * 16 > a.R) return;    // not a row block of this code width
     const int strip0 = (row_block * WAVES + wave) * SPW;
     const uint8_t* mat = mat_e + size_t(strip0) * NSB * SBB;

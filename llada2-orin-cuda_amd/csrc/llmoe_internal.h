@@ -110,7 +110,27 @@ __device__ __forceinline__ float exp_f32(float x) {
     return x != x ? x : v;
 }
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + exp_f32(-x)); }
-__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + exp_f32(-x)); }
+// SiLU of the gate_up epilogue, whose result is multiplied by u and rounded to fp16 (2^-11): exp(-g) by a
+// Cody-Waite reduction with one ln2 constant and a degree-5 Taylor polynomial (relative error < 1e-5), scaled
+// exactly by ldexp; 1 / (1 + e) by three Newton steps from a bit-pattern seed. The exp argument is clamped to
+// [-104, 80] (beyond it the fp16 product no longer changes), which keeps every step finite. IEEE fma / mul / add /
+// rint / min / max / ldexp only, the same sequence as the CPU checker's orc_silu.
+__device__ __forceinline__ float silu_f32(float g) {
+    const float x = fminf(fmaxf(-g, -104.0f), 80.0f);
+    const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+    const float r = __builtin_fmaf(n, -0.693147182464599609375f, x);
+    float p = 8.33333376795053482055664062500e-03f;
+    p = __builtin_fmaf(p, r, 4.16666679084300994873046875000e-02f);
+    p = __builtin_fmaf(p, r, 1.66666671633720397949218750000e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const float d = 1.0f + __builtin_ldexpf(p, int(n));
+    float q = __int_as_float(0x7EF311C3 - __float_as_int(d));
+#pragma unroll
+    for (int i = 0; i < 3; ++i) q = __builtin_fmaf(q, __builtin_fmaf(-d, q, 1.0f), q);
+    return g * q;
+}
 
 // fp32 -> fp16 with round-to-nearest-even on exact ties, in integer ops. (Measured on gfx950: v_cvt_f16_f32
 // does not round every exact halfway case to even, so the hardware conversion is not used.)

@@ -63,7 +63,24 @@ float orc_exp(float x) {
 }
 
 float orc_sigmoid(float x) { return 1.0f / (1.0f + orc_exp(-x)); }
-float orc_silu(float x) { return x / (1.0f + orc_exp(-x)); }
+/* SiLU of the gate_up epilogue (its result is multiplied by u and rounded to fp16): exp(-g) by Cody-Waite with one
+ * ln2 constant and a degree-5 Taylor polynomial, exact scaling by ldexp, 1 / (1 + e) by three Newton steps from a
+ * bit-pattern seed; the exp argument clamped to [-104, 80], which keeps every step finite. */
+float orc_silu(float g) {
+    const float x = fminf(fmaxf(-g, -104.0f), 80.0f);
+    const float n = rintf(x * 1.44269502162933349609375f);
+    const float r = fmaf(n, -0.693147182464599609375f, x);
+    float p = 8.33333376795053482055664062500e-03f;           /* 1/5! */
+    p = fmaf(p, r, 4.16666679084300994873046875000e-02f);      /* 1/4! */
+    p = fmaf(p, r, 1.66666671633720397949218750000e-01f);      /* 1/3! */
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const float d = 1.0f + ldexpf(p, (int)n);
+    float q = bits_f(0x7EF311C3u - f_bits(d));
+    for (int i = 0; i < 3; ++i) q = fmaf(q, fmaf(-d, q, 1.0f), q);
+    return g * q;
+}
 
 /* fp32 -> fp16, round to nearest even, overflow to inf, subnormals kept. */
 uint16_t orc_f32_to_f16(float f) {

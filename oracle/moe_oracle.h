@@ -5,8 +5,8 @@
  * __graft_entry__.py and bench.py's cpu_baseline leg may load it; the product (libllmoe.so) never links or
  * calls it. Every function restates the reference algorithm it cites (paths relative to the reference repo
  * patrickbdevaney/llada2-orin-cuda) in plain C, with one deliberate difference that is shared with the GPU
- * product: transcendental functions are this file's own (orc_exp), so the GPU can reproduce every fp32
- * operation bit for bit.
+ * product: transcendental functions are this file's own (orc_exp for the routing sigmoid, orc_silu for the
+ * gate_up epilogue), so the GPU can reproduce every fp32 operation bit for bit.
  *
  * Floating-point contract shared with the GPU kernels (compile with -ffp-contract=off):
  *   - every add / mul / div is an IEEE fp32 op, fused multiply-adds only where written as fmaf();
