@@ -137,9 +137,9 @@ __device__ __forceinline__ float silu_f32(float g) {
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     const uint32_t x = __float_as_uint(f);
     const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
-    const uint32_t mant = ax & 0x7fffffu, rem = mant & 0x1fffu;
-    uint32_t hn = (((ax >> 23) - 112u) << 10) | (mant >> 13);                      // normal half
-    hn += (rem > 0x1000u || (rem == 0x1000u && (hn & 1u))) ? 1u : 0u;
+    // normal half: round the 13 dropped mantissa bits to nearest even by adding 0xFFF plus the kept lsb (a carry
+    // runs into the exponent as it should), then rebias the exponent
+    const uint32_t hn = ((ax + 0xFFFu + ((ax >> 13) & 1u)) >> 13) - (112u << 10);
     // every active lane a normal half (the common case): done; otherwise every range's result is computed and
     // the one for ax selected
     if (__all(ax - 0x38800000u < 0x477ff000u - 0x38800000u)) return uint16_t(sign | hn);
