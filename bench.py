@@ -242,6 +242,51 @@ def measured_traffic():
     return None
 
 
+PROFILE_3_TRAFFIC = ROOT / "profiles" / "tiled_gemm_config3_traffic.txt"
+PROFILE_3_STATS = ROOT / "profiles" / "tiled_gemm_config3_kernel_stats.txt"
+
+
+def profile_column(path, kernel, col):
+    """Column `col` (0 = the kernel name) of the row for `kernel` in a committed rocprofv3 summary table, or None."""
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        f = line.split()
+        if f and f[0] == kernel and len(f) > col:
+            try:
+                return float(f[col])
+            except ValueError:
+                return None
+    return None
+
+
+def roofline_2048(c3):
+    """Weight-stream roofline of one config-3 layer (2048 tokens): the tiled gate_up + down GEMMs' algorithmic
+    weight bytes over their steady-state durations (HIP events on the launch stream, the 20 layers launched in
+    turn), the int8 MFMA rate of the same phase, and the HBM bytes the committed rocprofv3 summaries measured for the
+    two kernels (calibrated FETCH_SIZE + WRITE_SIZE per launch) against the algorithmic bytes."""
+    per_layer = c3["weight_bytes"] / c3["layers"]
+    t = (c3["gate_up_ms_per_layer"] + c3["down_ms_per_layer"]) * 1e-3
+    ops = 2 * c3["tokens"] * (K + 1) * 3 * I * H
+    gu_mb = profile_column(PROFILE_3_TRAFFIC, "tiled_gemm<0>", 4)
+    dn_mb = profile_column(PROFILE_3_TRAFFIC, "tiled_gemm<1>", 4)
+    traffic = None if gu_mb is None or dn_mb is None else (gu_mb + dn_mb) * 1e6
+    # algorithmic bytes of the two launches: weights, the gathered A8 rows of x (2 KB + 128 B per slot), Z written
+    # and Z' read (1 KB + 512 B and 512 B + 32 B per slot), Y written (8 KB per slot)
+    slots = c3["tokens"] * (K + 1)
+    algo = per_layer + slots * (2048 + 128 + 1024 + 544 + 8192)
+    gu_us = profile_column(PROFILE_3_STATS, "tiled_gemm<0>", 2)
+    dn_us = profile_column(PROFILE_3_STATS, "tiled_gemm<1>", 2)
+    achieved = per_layer / t / 1e9
+    return {"bound": "hbm", "kernel": "tiled_gemm<gate_up> + tiled_gemm<down> (config 3, one 2048-token layer)",
+            "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
+            "weight_bytes_per_layer": per_layer, "gate_up_ms": c3["gate_up_ms_per_layer"],
+            "down_ms": c3["down_ms_per_layer"], "int8_TOPS": ops / t / 1e12,
+            "int8_mfma_frac": ops / t / 1e12 / PEAK_INT8_TOPS, "traffic": traffic,
+            "algorithmic_bytes": algo, "traffic_ratio": None if traffic is None else traffic / algo,
+            "rocprof_avg_us": {"gate_up": gu_us, "down": dn_us}}
+
+
 def copy_calibration(torch, mib=512, reps=3):
     """Plain device copies of a known size, so counter runs can calibrate FETCH_SIZE / WRITE_SIZE per byte."""
     a = torch.empty(mib << 20, dtype=torch.uint8, device="cuda:0")
@@ -358,6 +403,17 @@ def cpu_baseline(L, x_np, pool, seconds):
                       f"(A8, fixed-order router, routing, integer W*A8 experts, FWHT-512, combine), {dt:.1f} s"}
 
 
+def prefill_steps(args, config):
+    """(timed steps, warm-up steps) of a prefill configuration: a share of --steps / --warmup with a floor, so that
+    the 2048- and 4096-token half of the metric is never timed from one or two steps (config 3 is a 20-layer stack
+    of ~5 ms per step, config 4 one layer of ~0.4-0.6 ms, config 2 one layer of ~0.13 ms)."""
+    if config == 3:
+        return max(5, args.steps // 20), max(2, args.warmup // 10)
+    if config == 4:
+        return max(10, args.steps // 20), max(3, args.warmup // 20)
+    return max(20, args.steps // 5), max(5, args.warmup // 10)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -388,17 +444,17 @@ def main():
 
     if args.only:
         if args.only == "config2":
-            r = prefill_config(llmoe, synth, torch, "config 2", 512, "mixed", True, 48, None, max(2, args.steps // 10), 2,
+            r = prefill_config(llmoe, synth, torch, "config 2", 512, "mixed", True, 48, None, *prefill_steps(args, 2),
                                nlayers=4, outliers=0.01)
         else:
             bits = int(args.only[-1])
             r = [prefill_config(llmoe, synth, torch, f"config 4: {bits}-bit {kind}", 4096, bits, False, 256, kind,
-                                max(2, args.steps // 40), 1, nlayers=1 if bits == 8 else 2)
+                                *prefill_steps(args, 4), nlayers=1 if bits == 8 else 2)
                  for kind in ("uniform", "skewed")]
         print(json.dumps(r))
         return
     if args.only_stack:
-        print(json.dumps(stack_config(llmoe, synth, torch, max(1, args.steps // 20), max(1, args.warmup // 10))))
+        print(json.dumps(stack_config(llmoe, synth, torch, *prefill_steps(args, 3))))
         return
     log("[bench] config 1 (headline)")
     c1, (L1, G1s, x1, _, _) = one_layer_config(llmoe, synth, torch, "config 1: 32 tokens, mixed 2/3/4-bit + W8A8 "
@@ -406,6 +462,7 @@ def main():
                                               1, 32, "mixed", True, 256, args.steps, args.warmup, zero_bias=True)
     c1["with_combine_norm"] = norm_step(llmoe, torch, G1s, x1, args.steps, args.warmup)
     configs = [c1]
+    c3 = None
     if not args.only_headline:
         log("[bench] config 0")
         c0, (_, G0s, _, _, _) = one_layer_config(llmoe, synth, torch, "config 0: 32 tokens, 4-bit, pool 48, "
@@ -417,9 +474,10 @@ def main():
         log("[bench] config 2")
         configs.append(prefill_config(llmoe, synth, torch, "config 2: 512 tokens, mixed 2/3/4-bit + W8A8 shared, "
                                       "router x Wr with 1% outlier channels x20, block pool 48", 512, "mixed", True,
-                                      48, None, max(2, args.steps // 10), 2, nlayers=4, outliers=0.01))
+                                      48, None, *prefill_steps(args, 2), nlayers=4, outliers=0.01))
         log("[bench] config 3")
-        configs.append(stack_config(llmoe, synth, torch, max(1, args.steps // 20), max(1, args.warmup // 10)))
+        c3 = stack_config(llmoe, synth, torch, *prefill_steps(args, 3))
+        configs.append(c3)
         for T in (32, 2048):
             log(f"[bench] dense projection, {T} tokens")
             configs.append(dense_config(llmoe, synth, torch, 3072, 8, T, max(5, args.steps // 4), 5))
@@ -428,7 +486,7 @@ def main():
                 log(f"[bench] config 4: {bits}-bit {kind}")
                 configs.append(prefill_config(llmoe, synth, torch, f"config 4: 4096 tokens, all experts {bits}-bit, "
                                               f"{kind} routing, no shared expert", 4096, bits, False, 256, kind,
-                                              max(2, args.steps // 40), 1, nlayers=1 if bits == 8 else 2))
+                                              *prefill_steps(args, 4), nlayers=1 if bits == 8 else 2))
 
     p = c1["stage_ms"]
     gu_s = p["gate_up"] * 1e-3
@@ -454,7 +512,8 @@ def main():
         "config": {"workload": c1["workload"], "tokens": 32, "hidden": H, "inter": I, "experts": E, "top_k": K,
                    "parallelism": "single GPU"},
         "weight_stream_GBps": c1["weight_stream_GBps"], "weight_stream_frac_peak": c1["weight_stream_frac_peak"],
-        "roofline": roofline, "cpu_baseline": cpu, "configs": configs,
+        "roofline": roofline, "roofline_2048": roofline_2048(c3) if c3 else None, "cpu_baseline": cpu,
+        "configs": configs,
     }
     print(json.dumps(line))
 

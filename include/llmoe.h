@@ -124,9 +124,10 @@ int llmoe_layer_forward(llmoe_layer* layer, const float* x, const float* logits,
                         llmoe_stream stream);
 
 /* Numerics of a layer's expert stage (default LLMOE_NUMERICS_EXACT).
- *   EXACT: every stage follows one fixed fp32 operation sequence (SiLU with a polynomial exp and a correctly rounded
- *          divide, integer round-to-nearest-even to fp16), so results are bit-identical run to run and to the CPU
- *          restatement of the reference.
+ *   EXACT: every stage follows one fixed fp32 operation sequence, so results are bit-identical run to run and to
+ *          the CPU restatement of the reference. The routing sigmoid uses a degree-7 polynomial exp and a correctly
+ *          rounded divide; the gate_up SiLU a degree-5 polynomial exp with exact ldexp scaling and a reciprocal by
+ *          three Newton steps; fp32 -> fp16 is integer round-to-nearest-even.
  *   FAST:  the SiLU of gate_up uses the hardware exp, reciprocal and fp16 conversion -- the precision of the
  *          reference's own __expf / __fdividef / __float2half (engine/moe_i8.cu:221). Z then differs from EXACT by
  *          at most one fp16 rounding step; the int32 expert products and every later stage are computed exactly as
@@ -186,7 +187,9 @@ int llmoe_layer_stage_ms(llmoe_layer* layer, float* ms);
 /* Re-launch one expert stage of the latest llmoe_experts / llmoe_experts_norm call (LLMOE_STAGE_GATE_UP, _FWHT,
  * _DOWN or _COMBINE) `reps` times back to back between two HIP events on `stream`, and return the average
  * milliseconds per launch (the kernel's steady-state duration). The stages are idempotent except the combine of
- * an llmoe_experts_norm call, which adds into h again on every repeat. Waits for completion. */
+ * an llmoe_experts_norm call, which adds into h again on every repeat. Waits for completion. When the latest call
+ * had one routing block (T <= block), FWHT-512 + A8 ran inside the down GEMM: LLMOE_STAGE_FWHT then returns
+ * LLMOE_ESTATE and its cost is part of LLMOE_STAGE_DOWN. */
 int llmoe_layer_time_stage(llmoe_layer* layer, int stage, int reps, llmoe_stream stream, float* avg_ms);
 
 /* As llmoe_layer_time_stage over n layers launched in turn (layer 0, 1, .., n-1, repeated `reps` times): with

@@ -206,6 +206,44 @@ int plan_and_place(llmoe_layer* L, const int32_t* topk, const float* topw, int T
 
 }  // namespace
 
+namespace {
+// Intermediates of llmoe_experts_scratch: one file-scope device array per GPU, sized for LLMOE_SCRATCH_MAX_TOKENS
+// tokens of K <= 8 routed slots plus the shared slot. Regions (256-byte aligned): Z fp16 [S, 512], zq int8 [S, 512],
+// zs fp32 [S, 4], zsum int32 [S, 4], Y fp32 [S, 2048].
+constexpr size_t SCR_S = size_t(LLMOE_SCRATCH_MAX_TOKENS) * 9;
+constexpr size_t SCR_Z = 0;
+constexpr size_t SCR_ZQ = SCR_Z + SCR_S * 512 * 2;
+constexpr size_t SCR_ZS = SCR_ZQ + SCR_S * 512;
+constexpr size_t SCR_ZSUM = SCR_ZS + SCR_S * 4 * 4;
+constexpr size_t SCR_Y = SCR_ZSUM + SCR_S * 4 * 4;
+constexpr size_t SCR_BYTES = SCR_Y + SCR_S * 2048 * 4;
+static_assert(SCR_ZQ % 256 == 0 && SCR_ZS % 256 == 0 && SCR_ZSUM % 256 == 0 && SCR_Y % 256 == 0, "alignment");
+static_assert(SCR_BYTES == LLMOE_SCRATCH_BYTES, "LLMOE_SCRATCH_BYTES in llmoe.h");
+
+static __device__ __align__(256) uint8_t scratch[SCR_BYTES];
+
+constexpr int SCR_MAX_DEV = 64;
+std::mutex g_scr_mu;
+uint8_t* g_scr_ptr[SCR_MAX_DEV] = {};   // device address of `scratch` on each GPU (the host symbol is a stand-in)
+
+// the device address of `scratch` on the current GPU, looked up once per GPU by llmoe_layer_create (so that a
+// later llmoe_experts_scratch call, possibly under graph capture, makes no runtime lookup)
+int scratch_ptr(uint8_t** out) {
+    int dev = 0;
+    HIPCHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= SCR_MAX_DEV) return fail(LLMOE_EINVAL, "device %d beyond the scratch table", dev);
+    std::lock_guard<std::mutex> lk(g_scr_mu);
+    if (!g_scr_ptr[dev]) {
+        void* p = nullptr;
+        HIPCHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(LLMOE_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+        g_scr_ptr[dev] = static_cast<uint8_t*>(p);
+    }
+    *out = g_scr_ptr[dev];
+    return LLMOE_OK;
+}
+}  // namespace
+
 extern "C" {
 
 const char* llmoe_last_error(void) { return g_err.c_str(); }
@@ -238,6 +276,8 @@ int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t bl
             return fail(LLMOE_EINVAL, "expert %d: matrix beyond the blob (%zu bytes)", e, blob_bytes);
     }
     if (int rc = llmoe::ensure_gemm_setup()) return rc;
+    uint8_t* scr = nullptr;
+    if (int rc = scratch_ptr(&scr)) return rc;
 
     llmoe_layer* L = new (std::nothrow) llmoe_layer();
     if (!L) return fail(LLMOE_ENOMEM, "host allocation");
@@ -516,41 +556,6 @@ int llmoe_experts_norm(llmoe_layer* L, const int8_t* xq, const float* xs, const 
 
 }  // extern "C"
 
-namespace {
-// Intermediates of llmoe_experts_scratch: one file-scope device array per GPU, sized for LLMOE_SCRATCH_MAX_TOKENS
-// tokens of K <= 8 routed slots plus the shared slot. Regions (256-byte aligned): Z fp16 [S, 512], zq int8 [S, 512],
-// zs fp32 [S, 4], zsum int32 [S, 4], Y fp32 [S, 2048].
-constexpr size_t SCR_S = size_t(LLMOE_SCRATCH_MAX_TOKENS) * 9;
-constexpr size_t SCR_Z = 0;
-constexpr size_t SCR_ZQ = SCR_Z + SCR_S * 512 * 2;
-constexpr size_t SCR_ZS = SCR_ZQ + SCR_S * 512;
-constexpr size_t SCR_ZSUM = SCR_ZS + SCR_S * 4 * 4;
-constexpr size_t SCR_Y = SCR_ZSUM + SCR_S * 4 * 4;
-constexpr size_t SCR_BYTES = SCR_Y + SCR_S * 2048 * 4;
-static_assert(SCR_ZQ % 256 == 0 && SCR_ZS % 256 == 0 && SCR_ZSUM % 256 == 0 && SCR_Y % 256 == 0, "alignment");
-static_assert(SCR_BYTES == LLMOE_SCRATCH_BYTES, "LLMOE_SCRATCH_BYTES in llmoe.h");
-
-static __device__ __align__(256) uint8_t scratch[SCR_BYTES];
-
-constexpr int SCR_MAX_DEV = 64;
-std::mutex g_scr_mu;
-uint8_t* g_scr_ptr[SCR_MAX_DEV] = {};   // device address of `scratch` on each GPU (the host symbol is a stand-in)
-
-int scratch_ptr(uint8_t** out) {
-    int dev = 0;
-    HIPCHECK(hipGetDevice(&dev));
-    if (dev < 0 || dev >= SCR_MAX_DEV) return fail(LLMOE_EINVAL, "device %d beyond the scratch table", dev);
-    std::lock_guard<std::mutex> lk(g_scr_mu);
-    if (!g_scr_ptr[dev]) {
-        void* p = nullptr;
-        HIPCHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-        if (!p) return fail(LLMOE_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
-        g_scr_ptr[dev] = static_cast<uint8_t*>(p);
-    }
-    *out = g_scr_ptr[dev];
-    return LLMOE_OK;
-}
-}  // namespace
 
 extern "C" {
 
@@ -618,7 +623,10 @@ hipError_t relaunch_stage(llmoe_layer* L, int stage, hipStream_t st) {
     switch (stage) {
         case LLMOE_STAGE_GATE_UP: return launch_gemm(GEMM_GATE_UP, L->last_gu, L->last_tgu, L->last_tiled, st);
         case LLMOE_STAGE_DOWN: return launch_gemm(GEMM_DOWN, L->last_dn, L->last_tdn, L->last_tiled, st);
-        case LLMOE_STAGE_FWHT: return launch_fwht_a8(L->last_w.Z, L->last_S, L->last_w.zq, L->last_w.zs, L->last_w.zsum, st);
+        case LLMOE_STAGE_FWHT:
+            // one routing block: FWHT-512 + A8 runs inside the streamed down GEMM (its time is in that stage)
+            if (!L->last_tiled) return hipErrorNotSupported;
+            return launch_fwht_a8(L->last_w.Z, L->last_S, L->last_w.zq, L->last_w.zs, L->last_w.zsum, st);
         case LLMOE_STAGE_COMBINE:
             if (L->last_norm.h)   // re-adds into h: each repeat moves the residual stream on by one more layer
                 return launch_combine_norm(L->last_w.Y, L->tok_slots, L->last_T, d.top_k + (d.has_shared ? 1 : 0),
@@ -640,6 +648,9 @@ int llmoe_layers_time_stage(llmoe_layer* const* layers, int n, int stage, int re
     for (int i = 0; i < n; ++i) {
         if (int rc = check_layer(layers[i])) return rc;
         if (!layers[i]->have_last) return fail(LLMOE_ESTATE, "layer %d: no llmoe_experts call to repeat", i);
+        if (stage == LLMOE_STAGE_FWHT && !layers[i]->last_tiled)
+            return fail(LLMOE_ESTATE, "layer %d: at one routing block FWHT-512 + A8 is fused into the down GEMM "
+                                      "(time LLMOE_STAGE_DOWN)", i);
     }
     const hipStream_t st = static_cast<hipStream_t>(stream);
     hipEvent_t a, b;

@@ -256,7 +256,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, con
         Step<BITS>& cur = ring[u % D];
         constexpr int sb = u % NSB;
         const int strip = strip0 + u / NSB;
+        // the wave's meta slot: lanes 0-47 store the superblock's 192 bytes, then every lane reads other lanes'
+        // bytes. A wave's LDS operations execute in program order; the wave barriers keep the compiler from moving
+        // this step's store above the previous step's reads or the reads above the store.
+        __builtin_amdgcn_wave_barrier();
         if (lane < META_SB / 4) *reinterpret_cast<uint32_t*>(mp + 4 * lane) = cur.m;
+        __builtin_amdgcn_wave_barrier();
         const u4 ms0 = *reinterpret_cast<const u4*>(mp + 32 * q);
         const u4 ms1 = *reinterpret_cast<const u4*>(mp + 32 * q + 16);
         const u4 zw4 = *reinterpret_cast<const u4*>(mp + 128 + 16 * q);

@@ -272,13 +272,6 @@ struct DecodeState {
 };
 
 // Slots and work units of the decode step (engine/ops.cu:333-370), one workgroup of 256 threads.
-#ifdef LLMOE_TILED_TRACE
-// timing builds only: s_memrealtime at the planner's phase boundaries
-__device__ unsigned long long g_plan_trace[16];
-#define PLAN_TRACE(k) if (threadIdx.x == 0) g_plan_trace[k] = __builtin_amdgcn_s_memrealtime()
-#else
-#define PLAN_TRACE(k) ((void)0)
-#endif
 
 // Slots: expert-major, token-ascending; shared slots T K + t. Units: items of 16 slots split into row blocks by
 // code width, longest first (2 / 3 / 4 / 8-bit experts, then the shared expert).
@@ -505,7 +498,6 @@ __global__ void __launch_bounds__(PLAN_NT) plan_kernel(const uint32_t* __restric
     const int tid = threadIdx.x, e = tid % MAXE, part = tid / MAXE, nb = (T + block - 1) / block;
     const int lane = tid & 63, wv = tid >> 6, w = wv & 3;   // (w: the wave within the expert-scan group)
     const bool g0 = part == 0;                 // the expert's lead thread (scans, units)
-    PLAN_TRACE(0);
     // token masks of the part's block range [b_lo, b_hi): unconditional loads at clamped indices, so that the
     // batch is issued back to back
     const int ec = min(e, E - 1), nbp = (nb + NP - 1) / NP, b_lo = min(nb, part * nbp), b_hi = min(nb, b_lo + nbp);
@@ -534,7 +526,6 @@ __global__ void __launch_bounds__(PLAN_NT) plan_kernel(const uint32_t* __restric
         cbefore += pp < part ? v : 0;
         c += v;
     }
-    PLAN_TRACE(1);
     const bool big = e < E && tiled && c > 0;
     const bool sbig = has_shared && tiled;
     const int nsch = sbig ? tiled_chunks(T) : 0;
@@ -637,7 +628,6 @@ __global__ void __launch_bounds__(PLAN_NT) plan_kernel(const uint32_t* __restric
         n_units[2] = bt;
         n_units[3] = bt;
     }
-    PLAN_TRACE(2);
     if (!tiled) return;
     // the tiled chunks: tiled_per(c) slots of an expert's c each, the last one shorter (Item.rb unused)
     __syncthreads();
@@ -683,7 +673,6 @@ __global__ void __launch_bounds__(PLAN_NT) plan_kernel(const uint32_t* __restric
         pre_dn[n] = inc1;
     }
     __syncthreads();
-    PLAN_TRACE(3);
     // work partition: workgroup q starts at task position lo_q = ceil(q C / G); the chunk j holding it
     // (pre[j] <= lo_q < pre[j + 1]) is found by binary search, and the task inside it is the first row block
     // whose cost span (after the chunk's staging cost) starts at or after lo_q (one past the chunk's last: the
@@ -713,7 +702,6 @@ __global__ void __launch_bounds__(PLAN_NT) plan_kernel(const uint32_t* __restric
             ts[q] = r >= nrb ? a + 1 : (a | (r << TASK_RB_SHIFT));
         }
     }
-    PLAN_TRACE(4);
 }
 
 // Place every (token, k) pair in its slot; tok_slots[t, K] = the shared slot (or -1). grid nb, 256 threads.
@@ -854,9 +842,3 @@ hipError_t launch_place(const int32_t* topk, const float* topw, uint32_t* mask, 
 }
 
 }  // namespace llmoe
-
-#ifdef LLMOE_TILED_TRACE
-extern "C" int llmoe_plan_trace(void* host) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(llmoe::g_plan_trace), 16 * 8) == hipSuccess ? 0 : -1;
-}
-#endif

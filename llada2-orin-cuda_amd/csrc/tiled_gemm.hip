@@ -432,29 +432,15 @@ __device__ __forceinline__ void rowblock_store(const GemmArgs& a, const Item& it
     }
 }
 
-#ifdef LLMOE_TILED_TRACE
-// timing build only: per unit, [start, staged, end, unit | expert << 20 | hw_id << 32] in the 100 MHz clock
-constexpr int TRACE_MAX = 1 << 16;
-__device__ unsigned long long g_trace[TRACE_MAX * 4];
-__device__ __forceinline__ void trace_put(int slot, unsigned long long v) {
-    if (threadIdx.x == 0 && slot < TRACE_MAX * 4) g_trace[slot] = v;
-}
-#define TRACE_AT(u, k) trace_put(4 * (u) + (k), __builtin_amdgcn_s_memrealtime())
-#else
-#define TRACE_AT(u, k) ((void)0)
-#endif
-
 template <int BITS, int MODE, int NTILE>
 __device__ __forceinline__ void tiled_body(const GemmArgs& a, const Item& it, const uint8_t* mat, uint8_t* lds,
-                                           int rb0, int rb1, int u) {
+                                           int rb0, int rb1) {
     constexpr int K = MODE == GEMM_DOWN ? 512 : 2048;
-    (void)u;
     // row block rb + 1's first weights are requested between rb's products and rb's stores: the weight loads then
     // precede the output stores in the in-order memory counter, so waiting for them never waits for the stores
     RowRegs<BITS, MODE> r;
     rowblock_load<BITS, MODE, NTILE>(mat, rb0, r);
     stage_chunk<K>(a, it, lds);
-    TRACE_AT(u, 1);
     for (int rb = rb0; rb < rb1; ++rb) {
         float acc[RowRegs<BITS, MODE>::S][NTILE][4];
         rowblock_compute<BITS, MODE, NTILE>(mat, lds, rb, r, acc);
@@ -480,7 +466,6 @@ __global__ void __launch_bounds__(nthreads_for(MODE == GEMM_DOWN ? 512 : 2048)) 
     const int p = G % NXCD ? int(blockIdx.x) : int(blockIdx.x % NXCD) * (G / NXCD) + int(blockIdx.x / NXCD);
     const int s0 = *const_ptr(a.tstart + p), s1 = *const_ptr(a.tstart + p + 1);
     const int c0 = s0 & CMASK, r0 = s0 >> TASK_RB_SHIFT, c1 = s1 & CMASK, r1 = s1 >> TASK_RB_SHIFT;
-    int u = p * 16;   // trace slot (timing builds)
     for (int c = c0; c < c1 || (c == c1 && r1 > 0); ++c) {
         // the chunk, and the expert's matrix offset and code width together, by scalar loads (the lists are
         // written by earlier kernels only)
@@ -495,37 +480,30 @@ __global__ void __launch_bounds__(nthreads_for(MODE == GEMM_DOWN ? 512 : 2048)) 
                                            : tiled_row_blocks(MODE == GEMM_DOWN, bits);
         const int rb0 = c == c0 ? r0 : 0, rb1 = c == c1 ? r1 : nrb;
         if (rb0 >= rb1) continue;
-#ifdef LLMOE_TILED_TRACE
-        TRACE_AT(u, 0);
-        trace_put(4 * u + 3, (unsigned long long)((c & 0xFFFF) | ((rb1 - rb0) << 16) | (((it.ntok + 15) >> 4) << 22) |
-                                                  (bits << 25)) | ((unsigned long long)it.expert << 32));
-#endif
         // token tiles actually present (a chunk has <= 64 slots; absent tiles are not computed)
         const int nt = (it.ntok + 15) >> 4;
         if (nt > 3) {
-            if (bits == 2) tiled_body<2, MODE, 4>(a, it, mat, lds, rb0, rb1, u);
-            else if (bits == 3) tiled_body<3, MODE, 4>(a, it, mat, lds, rb0, rb1, u);
-            else if (bits == 4) tiled_body<4, MODE, 4>(a, it, mat, lds, rb0, rb1, u);
-            else tiled_body<8, MODE, 4>(a, it, mat, lds, rb0, rb1, u);
+            if (bits == 2) tiled_body<2, MODE, 4>(a, it, mat, lds, rb0, rb1);
+            else if (bits == 3) tiled_body<3, MODE, 4>(a, it, mat, lds, rb0, rb1);
+            else if (bits == 4) tiled_body<4, MODE, 4>(a, it, mat, lds, rb0, rb1);
+            else tiled_body<8, MODE, 4>(a, it, mat, lds, rb0, rb1);
         } else if (nt == 3) {
-            if (bits == 2) tiled_body<2, MODE, 3>(a, it, mat, lds, rb0, rb1, u);
-            else if (bits == 3) tiled_body<3, MODE, 3>(a, it, mat, lds, rb0, rb1, u);
-            else if (bits == 4) tiled_body<4, MODE, 3>(a, it, mat, lds, rb0, rb1, u);
-            else tiled_body<8, MODE, 3>(a, it, mat, lds, rb0, rb1, u);
+            if (bits == 2) tiled_body<2, MODE, 3>(a, it, mat, lds, rb0, rb1);
+            else if (bits == 3) tiled_body<3, MODE, 3>(a, it, mat, lds, rb0, rb1);
+            else if (bits == 4) tiled_body<4, MODE, 3>(a, it, mat, lds, rb0, rb1);
+            else tiled_body<8, MODE, 3>(a, it, mat, lds, rb0, rb1);
         } else if (nt == 2) {
-            if (bits == 2) tiled_body<2, MODE, 2>(a, it, mat, lds, rb0, rb1, u);
-            else if (bits == 3) tiled_body<3, MODE, 2>(a, it, mat, lds, rb0, rb1, u);
-            else if (bits == 4) tiled_body<4, MODE, 2>(a, it, mat, lds, rb0, rb1, u);
-            else tiled_body<8, MODE, 2>(a, it, mat, lds, rb0, rb1, u);
+            if (bits == 2) tiled_body<2, MODE, 2>(a, it, mat, lds, rb0, rb1);
+            else if (bits == 3) tiled_body<3, MODE, 2>(a, it, mat, lds, rb0, rb1);
+            else if (bits == 4) tiled_body<4, MODE, 2>(a, it, mat, lds, rb0, rb1);
+            else tiled_body<8, MODE, 2>(a, it, mat, lds, rb0, rb1);
         } else {
-            if (bits == 2) tiled_body<2, MODE, 1>(a, it, mat, lds, rb0, rb1, u);
-            else if (bits == 3) tiled_body<3, MODE, 1>(a, it, mat, lds, rb0, rb1, u);
-            else if (bits == 4) tiled_body<4, MODE, 1>(a, it, mat, lds, rb0, rb1, u);
-            else tiled_body<8, MODE, 1>(a, it, mat, lds, rb0, rb1, u);
+            if (bits == 2) tiled_body<2, MODE, 1>(a, it, mat, lds, rb0, rb1);
+            else if (bits == 3) tiled_body<3, MODE, 1>(a, it, mat, lds, rb0, rb1);
+            else if (bits == 4) tiled_body<4, MODE, 1>(a, it, mat, lds, rb0, rb1);
+            else tiled_body<8, MODE, 1>(a, it, mat, lds, rb0, rb1);
         }
         __syncthreads();   // the next chunk re-stages the activations
-        TRACE_AT(u, 2);
-        ++u;
     }
 }
 
@@ -578,15 +556,3 @@ hipError_t launch_tiled_gemm(int mode, const GemmArgs& a, hipStream_t st) {
 }
 
 }  // namespace llmoe
-
-#ifdef LLMOE_TILED_TRACE
-extern "C" int llmoe_tiled_trace(void* host, size_t bytes, int clear) {
-    if (hipMemcpyFromSymbol(host, HIP_SYMBOL(llmoe::g_trace), bytes) != hipSuccess) return -1;
-    if (clear) {
-        void* p = nullptr;
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(llmoe::g_trace)) != hipSuccess) return -1;
-        if (hipMemset(p, 0, bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) return -1;
-    }
-    return 0;
-}
-#endif

@@ -15,7 +15,9 @@ import oracle
 from llmoe import Layer, synth
 
 sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+sys.path.insert(0, str(Path(__file__).resolve().parent))
 import gen  # noqa: E402
+from stages_f64 import check_stages_f64  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -162,6 +164,13 @@ def test_layer_forward_matches_oracle(gpu, T, mix, shared, pool):
     assert np.array_equal(out.view(np.uint32), r["out"].view(np.uint32)), "combine not bit-exact"
     ref64 = oracle.Layer(L).reference_f64(x, r["topk"], r["topw"])
     assert np.linalg.norm(out - ref64) / np.linalg.norm(ref64) < 5e-3   # engine/tests/test_moe_i8.cu:173
+    # each fp stage of the GPU's own data at max-abs 1e-3 relative against fp64 (gate_up epilogue + SiLU, FWHT + A8,
+    # down + combine)
+    S = T * 8 + (T if shared else 0)
+    check_stages_f64(L, G.read("xq", (T, 2048), np.int8), G.read("xs", (T, 16), np.float32), r["topk"], r["topw"],
+                     G.read("tok_slots", (T, 9), np.int32), G.read("Z", (S, 512), np.uint16),
+                     G.read("zq", (S, 512), np.int8), G.read("zs", (S, 4), np.float32), out,
+                     sorted({0, T // 2, T - 1}))
     G.close()
 
 
@@ -234,7 +243,11 @@ def test_tiled_units_bit_exact(gpu, T, mix, kind):
     (512, "mixed", True, 48, None),       # config 2: router x Wr with outlier channels, block pool 48
     (2048, "mixed", True, 256, "zipf"),   # one layer of config 3
     (4096, 2, False, 256, "uniform"),     # config 4, 2-bit
-    (4096, 8, False, 256, "skewed"),      # config 4, 8-bit, 16 experts take half the slots
+    (4096, 2, False, 256, "skewed"),      # config 4, 2-bit, 16 experts take half the slots
+    (4096, 4, False, 256, "uniform"),     # config 4, 4-bit
+    (4096, 4, False, 256, "skewed"),
+    (4096, 8, False, 256, "uniform"),     # config 4, 8-bit (W8A8)
+    (4096, 8, False, 256, "skewed"),
     (5120, 4, False, 256, "uniform"),     # 160 routing blocks: more block masks than the planner holds in registers
 ])
 def test_full_size_batch_invariance(gpu, T, mix, shared, pool, kind):

@@ -16,6 +16,8 @@ GOLD = Path(__file__).resolve().parent / "golden"
 import sys
 sys.path.insert(0, str(GOLD))
 import gen  # noqa: E402
+sys.path.insert(0, str(Path(__file__).resolve().parent))
+from stages_f64 import check_stages_f64  # noqa: E402
 
 
 def fixture(name):
@@ -227,9 +229,9 @@ def test_exp_sigmoid_silu_accuracy():
             assert abs(got - ref) <= 2.5 * np.spacing(np.float32(ref)), x
         s = 1.0 / (1.0 + math.exp(-x)) if x > -700 else 0.0
         assert abs(O.sigmoid(x) - s) <= 3e-7 * max(s, 1e-30) + 1e-45
-        # SiLU feeds an fp16 rounding (2^-11): degree-5 exp and a Newton reciprocal, within 1e-5; clamped exp
+        # SiLU feeds an fp16 rounding (2^-11): degree-5 exp and a Newton reciprocal, within 5e-6; clamped exp
         # argument below g = -80 (results under 1e-30)
-        assert abs(O.silu(x) - x * s) <= 1e-5 * abs(x * s) + 1e-30, x
+        assert abs(O.silu(x) - x * s) <= 5e-6 * abs(x * s) + 1e-30, x     # measured max 3.5e-6 over [-90, 110]
     assert O.exp(89.0) == math.inf
 
 
@@ -278,8 +280,12 @@ def test_experts_match_reference_gen_moe_case():
     ref = f["acc"].astype(np.float64)
     rel = np.linalg.norm(out - ref) / np.linalg.norm(ref)
     assert rel < 5e-3, rel                           # the reference's own bar (engine/tests/test_moe_i8.cu:173)
+    err = np.abs(out - ref).max() / np.abs(ref).max()
+    assert err <= 1e-3, err                          # the contract's max-abs 1e-3 relative
+    assert err <= 1e-5, err                          # what the fixture pins (measured 2.2e-7)
     f64 = L.reference_f64(x, idx, w)
     assert np.linalg.norm(f64 - ref) / np.linalg.norm(ref) < 5e-3
+    assert np.abs(f64 - ref).max() / np.abs(ref).max() <= 1e-5
 
 
 def test_experts_vs_fp64_with_shared():
@@ -289,6 +295,9 @@ def test_experts_vs_fp64_with_shared():
     r = L.forward(x, C=48)
     f64 = L.reference_f64(x, r["topk"], r["topw"])
     assert np.linalg.norm(r["out"] - f64) / np.linalg.norm(f64) < 5e-3
+    # every fp stage at max-abs 1e-3 relative against fp64 from the integer data the stage before produced
+    check_stages_f64(layer, r["xq"], r["xs"], r["topk"], r["topw"], r["tok_slots"], r["Z"], r["zq"], r["zs"],
+                     r["out"], range(8))
     # combine is the fixed-order sum of the weighted slot outputs
     acc = np.zeros_like(r["out"])
     for k in range(9):
