@@ -129,9 +129,12 @@ int llmoe_layer_forward(llmoe_layer* layer, const float* x, const float* logits,
  *          rounded divide; the gate_up SiLU a degree-5 polynomial exp with exact ldexp scaling and a reciprocal by
  *          three Newton steps; fp32 -> fp16 is integer round-to-nearest-even.
  *   FAST:  the SiLU of gate_up uses the hardware exp, reciprocal and fp16 conversion -- the precision of the
- *          reference's own __expf / __fdividef / __float2half (engine/moe_i8.cu:221). Z then differs from EXACT by
- *          at most one fp16 rounding step; the int32 expert products and every later stage are computed exactly as
- *          in EXACT from that Z, and the layer output agrees with EXACT within the contract's 1e-3 tolerance.
+ *          reference's own __expf / __fdividef / __float2half (engine/moe_i8.cu:221) -- and, with several routing
+ *          blocks (T > block), the down GEMM stores each slot output w acc rounded to fp16 (nearest even) for the
+ *          combine, which halves the slot outputs' HBM round trip (|w acc| must stay below 65504). Z then differs from EXACT by at most one fp16 rounding
+ *          step; the int32 expert products and every later stage are computed exactly as in EXACT from that Z (up to
+ *          the slot outputs' fp16 rounding), and the layer output agrees with EXACT within the contract's 1e-3
+ *          tolerance.
  * Takes effect from the next llmoe_experts / llmoe_experts_norm / llmoe_layer_forward call on the layer. */
 #define LLMOE_NUMERICS_EXACT 0
 #define LLMOE_NUMERICS_FAST 1
@@ -151,7 +154,9 @@ typedef struct {
                                                           n_items[0] / [1]: gate_up / down unit counts */
     uint16_t* Z;                                       /* fp16 SiLU(g) u               [S, I] */
     int8_t* zq; float* zs; int32_t* zsum;              /* A8(Z H512)                   [S, I], [S, I/128] */
-    float* Y;                                          /* weighted expert outputs      [S, H] */
+    float* Y;                                          /* weighted expert outputs      [S, H]
+                                                          (fp16 bits [S, H] after a LLMOE_NUMERICS_FAST call
+                                                          with T > block) */
     int ntok;                                          /* tokens per work item of the last dispatch */
     int max_items;                                     /* work-item capacity of the last dispatch */
 } llmoe_buffers;
@@ -166,6 +171,12 @@ int llmoe_layer_weight_bytes(const llmoe_layer* layer, size_t* bytes);
  * n <= 64. P int32 [n, R, Kw/128]. */
 int llmoe_group_products(llmoe_layer* layer, int expert, int which, const int8_t* xq, const int32_t* xsum, int n,
                          int32_t* P, llmoe_stream stream);
+
+/* Self-test of the device's fp32 -> fp16 conversion (test entry; no counterpart in the reference): every finite fp32
+ * bit pattern through the hardware conversion the kernels use (v_cvt_f16_f32) and through round-to-nearest-even
+ * spelled out in integer ops (the definition the CPU checker restates); *mismatches = the number of inputs on which
+ * they differ (0 on gfx950). Synchronous; takes a fraction of a second. */
+int llmoe_selftest_f16(uint64_t* mismatches);
 
 /* Per-stage timing (the analogue of Engine::mark / prof_collect, engine/engine.cu:385-407, enabled there by
  * PROF=1): while enabled, every stage of the layer's calls is bracketed by HIP events on the call's stream.

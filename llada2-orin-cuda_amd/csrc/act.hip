@@ -41,7 +41,20 @@ __global__ void __launch_bounds__(256) fwht_a8_kernel(const uint16_t* __restrict
 
 // out[t, :] = sum_{k < kk} Y[tok_slots[t, k], :], k ascending (engine/moe_i8.cu:505-515). grid (T, column slices).
 constexpr int MAX_KK = 9;   // top-8 + the shared expert
-__global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ Y, const int* __restrict__ tok_slots,
+// 4 consecutive slot outputs from element index i of Y: fp32, or fp16 bits (HALF, the fast-numerics down output)
+template <bool HALF>
+__device__ __forceinline__ float4 load_y4(const void* __restrict__ Y, size_t i) {
+    if constexpr (HALF) {
+        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(Y) + i);
+        return make_float4(f16_bits_to_f32(u.x & 0xFFFFu), f16_bits_to_f32(u.x >> 16), f16_bits_to_f32(u.y & 0xFFFFu),
+                           f16_bits_to_f32(u.y >> 16));
+    } else {
+        return *reinterpret_cast<const float4*>(static_cast<const float*>(Y) + i);
+    }
+}
+
+template <bool HALF>
+__global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ Y, const int* __restrict__ tok_slots,
                                                       int H, int kk, int K1, float* __restrict__ out) {
     const int t = blockIdx.x;
     // columns [h0, h1) of the row: gridDim.y slices, so that a small T still spreads over many CUs
@@ -58,7 +71,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
             const int h = hb + r * blockDim.x * 4;
 #pragma unroll
             for (int k = 0; k < MAX_KK; ++k)
-                if (k < kk && h < h1) v[r][k] = *reinterpret_cast<const float4*>(Y + size_t(sl[k]) * H + h);
+                if (k < kk && h < h1) v[r][k] = load_y4<HALF>(Y, size_t(sl[k]) * H + h);
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -125,7 +138,8 @@ __device__ __forceinline__ void fwht2048_ab(float (&x)[8], float* v) {
 // Sum of squares: thread i adds h[i + 256 j]^2 for j ascending, a 64-lane xor butterfly, then the 4 wave sums in
 // order -- the order the CPU checker uses.
 constexpr float INV_SQRT_2048 = 0.02209708691207961f;
-__global__ void __launch_bounds__(256) combine_norm_kernel(const float* __restrict__ Y, const int* __restrict__ tok_slots,
+template <bool HALF>
+__global__ void __launch_bounds__(256) combine_norm_kernel(const void* __restrict__ Y, const int* __restrict__ tok_slots,
                                                            int kk, int K1, const float* __restrict__ signs, float eps,
                                                            float* __restrict__ h, int8_t* __restrict__ q,
                                                            float* __restrict__ s, int* __restrict__ sum) {
@@ -139,9 +153,8 @@ __global__ void __launch_bounds__(256) combine_norm_kernel(const float* __restri
 #pragma unroll
     for (int k = 0; k < MAX_KK; ++k)
         if (k < kk) {
-            const float4* yp = reinterpret_cast<const float4*>(Y + size_t(sl[k]) * 2048 + 8 * i);
-            ya[k] = yp[0];
-            yb[k] = yp[1];
+            ya[k] = load_y4<HALF>(Y, size_t(sl[k]) * 2048 + 8 * i);
+            yb[k] = load_y4<HALF>(Y, size_t(sl[k]) * 2048 + 8 * i + 4);
         }
     float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -209,6 +222,29 @@ __global__ void __launch_bounds__(256) combine_norm_kernel(const float* __restri
 
 }  // namespace
 
+// f32_to_f16_rne against f32_to_f16_bits on fp32 bit patterns [start, start + n) (NaN patterns skipped): the
+// number of inputs on which they differ is added to *mismatches.
+__global__ void __launch_bounds__(256) f16_selftest_kernel(uint32_t start, uint32_t n,
+                                                           unsigned long long* __restrict__ mismatches) {
+    unsigned int bad = 0;
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u) {
+        const uint32_t b = start + i;
+        if ((b & 0x7fffffffu) > 0x7f800000u) continue;
+        const float f = __uint_as_float(b);
+        bad += f32_to_f16_rne(f) != f32_to_f16_bits(f) ? 1u : 0u;
+    }
+    if (bad) atomicAdd(mismatches, (unsigned long long)bad);
+}
+
+hipError_t launch_f16_selftest(unsigned long long* mismatches, hipStream_t st) {
+    for (uint32_t sign = 0; sign < 2; ++sign) {
+        f16_selftest_kernel<<<8192, 256, 0, st>>>(sign << 31, 0x7f800001u, mismatches);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 hipError_t launch_quant_a8(const float* x, int rows, int cols, int8_t* q, float* s, int* sum, hipStream_t st) {
     if (rows <= 0) return hipSuccess;
     const dim3 grid((cols / 512 + 3) / 4, rows);
@@ -222,20 +258,24 @@ hipError_t launch_fwht_a8(const uint16_t* Z, int nslots, int8_t* q, float* s, in
     return hipGetLastError();
 }
 
-hipError_t launch_combine_norm(const float* Y, const int* tok_slots, int T, int kk, int K1, const float* signs,
-                               float eps, float* h, int8_t* q, float* s, int* sum, hipStream_t st) {
+hipError_t launch_combine_norm(const void* Y, int yhalf, const int* tok_slots, int T, int kk, int K1,
+                               const float* signs, float eps, float* h, int8_t* q, float* s, int* sum, hipStream_t st) {
     if (T <= 0) return hipSuccess;
     if (kk > MAX_KK) return hipErrorInvalidValue;
-    combine_norm_kernel<<<T, 256, 0, st>>>(Y, tok_slots, kk, K1, signs, eps, h, q, s, sum);
+    if (yhalf) combine_norm_kernel<true><<<T, 256, 0, st>>>(Y, tok_slots, kk, K1, signs, eps, h, q, s, sum);
+    else combine_norm_kernel<false><<<T, 256, 0, st>>>(Y, tok_slots, kk, K1, signs, eps, h, q, s, sum);
     return hipGetLastError();
 }
 
-hipError_t launch_combine(const float* Y, const int* tok_slots, int T, int H, int kk, int K1, float* out,
+hipError_t launch_combine(const void* Y, int yhalf, const int* tok_slots, int T, int H, int kk, int K1, float* out,
                           hipStream_t st) {
     if (T <= 0) return hipSuccess;
     // a decode step's few rows are split over 8 column slices (256 columns, one pass of 64 threads x 2 float4)
     const int ns = T <= 256 && H % 256 == 0 ? H / 256 : 1;
-    combine_kernel<<<dim3(T, ns), ns > 1 ? 64 : 256, 0, st>>>(Y, tok_slots, H, kk, K1, out);
+    const dim3 grid(T, ns);
+    const int nth = ns > 1 ? 64 : 256;
+    if (yhalf) combine_kernel<true><<<grid, nth, 0, st>>>(Y, tok_slots, H, kk, K1, out);
+    else combine_kernel<false><<<grid, nth, 0, st>>>(Y, tok_slots, H, kk, K1, out);
     return hipGetLastError();
 }
 

@@ -124,6 +124,7 @@ struct llmoe_layer {
     Inter last_w{};
     int last_S = 0, last_T = 0, last_nt = 1;
     bool last_tiled = false;
+    bool last_yhalf = false;                        // the latest call's Y holds fp16 (fast numerics)
     bool have_last = false;
     std::vector<void*> allocs;
 
@@ -509,6 +510,10 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     g.slot_token = nullptr;
     g.xq = w.zq; g.xs = w.zs; g.xsum = w.zsum;
     g.K = I; g.R = H; g.Z = nullptr; g.Y = w.Y;
+    // fast numerics with several routing blocks: the slot outputs are rounded to fp16 (half the bytes through HBM
+    // for Y and the combine). A decode step's Y stays in the caches, where fp32 costs nothing more.
+    const bool yhalf = L->fast && L->tiled;
+    g.Yh = yhalf ? reinterpret_cast<uint16_t*>(w.Y) : nullptr;
     g.fast = 0;
     tg = g;
     g.zin = w.Z; g.xq_out = w.zq; g.xs_out = w.zs; g.xsum_out = w.zsum;
@@ -518,16 +523,17 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     L->last_dn = g;
     L->last_tdn = tg;
     L->last_S = S; L->last_T = T; L->last_tiled = L->tiled; L->last_out = out; L->last_norm = no; L->last_w = w;
+    L->last_yhalf = yhalf;
     L->have_last = true;
     L->mark(LLMOE_STAGE_DOWN, false, st);
     HIPCHECK(launch_gemm(GEMM_DOWN, g, tg, L->tiled, st));
     L->mark(LLMOE_STAGE_DOWN, true, st);
     L->mark(LLMOE_STAGE_COMBINE, false, st);
     if (no.h)
-        HIPCHECK(launch_combine_norm(w.Y, L->tok_slots, T, K + (d.has_shared ? 1 : 0), K + 1, no.signs, no.eps, no.h,
-                                     no.q, no.s, no.sum, st));
+        HIPCHECK(launch_combine_norm(w.Y, yhalf, L->tok_slots, T, K + (d.has_shared ? 1 : 0), K + 1, no.signs,
+                                     no.eps, no.h, no.q, no.s, no.sum, st));
     else
-        HIPCHECK(launch_combine(w.Y, L->tok_slots, T, H, K + (d.has_shared ? 1 : 0), K + 1, out, st));
+        HIPCHECK(launch_combine(w.Y, yhalf, L->tok_slots, T, H, K + (d.has_shared ? 1 : 0), K + 1, out, st));
     L->mark(LLMOE_STAGE_COMBINE, true, st);
     return LLMOE_OK;
 }
@@ -629,11 +635,12 @@ hipError_t relaunch_stage(llmoe_layer* L, int stage, hipStream_t st) {
             return launch_fwht_a8(L->last_w.Z, L->last_S, L->last_w.zq, L->last_w.zs, L->last_w.zsum, st);
         case LLMOE_STAGE_COMBINE:
             if (L->last_norm.h)   // re-adds into h: each repeat moves the residual stream on by one more layer
-                return launch_combine_norm(L->last_w.Y, L->tok_slots, L->last_T, d.top_k + (d.has_shared ? 1 : 0),
-                                           d.top_k + 1, L->last_norm.signs, L->last_norm.eps, L->last_norm.h,
-                                           L->last_norm.q, L->last_norm.s, L->last_norm.sum, st);
-            return launch_combine(L->last_w.Y, L->tok_slots, L->last_T, d.hidden, d.top_k + (d.has_shared ? 1 : 0),
-                                  d.top_k + 1, L->last_out, st);
+                return launch_combine_norm(L->last_w.Y, L->last_yhalf, L->tok_slots, L->last_T,
+                                           d.top_k + (d.has_shared ? 1 : 0), d.top_k + 1, L->last_norm.signs,
+                                           L->last_norm.eps, L->last_norm.h, L->last_norm.q, L->last_norm.s,
+                                           L->last_norm.sum, st);
+            return launch_combine(L->last_w.Y, L->last_yhalf, L->tok_slots, L->last_T, d.hidden,
+                                  d.top_k + (d.has_shared ? 1 : 0), d.top_k + 1, L->last_out, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -692,6 +699,20 @@ int llmoe_layer_weight_bytes(const llmoe_layer* L, size_t* bytes) {
     if (int rc = check_layer(L)) return rc;
     if (!bytes) return fail(LLMOE_EINVAL, "null argument");
     *bytes = L->weight_bytes;
+    return LLMOE_OK;
+}
+
+int llmoe_selftest_f16(uint64_t* mismatches) {
+    if (!mismatches) return fail(LLMOE_EINVAL, "null argument");
+    unsigned long long* d = nullptr;
+    HIPCHECK(hipMalloc(&d, sizeof(*d)));
+    hipError_t e = hipMemset(d, 0, sizeof(*d));
+    if (e == hipSuccess) e = launch_f16_selftest(d, nullptr);
+    unsigned long long h = 0;
+    if (e == hipSuccess) e = hipMemcpy(&h, d, sizeof(h), hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    if (e != hipSuccess) return fail(LLMOE_EHIP, "f16 self-test: %s", hipGetErrorString(e));
+    *mismatches = h;
     return LLMOE_OK;
 }
 

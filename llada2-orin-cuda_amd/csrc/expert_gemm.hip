@@ -385,14 +385,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, con
                             z0 = silu_mul_f16_fast(acc[nt][0], acc[nt][1]);
                             z1 = silu_mul_f16_fast(acc[nt][2], acc[nt][3]);
                         } else {
-                            z0 = f32_to_f16_bits(silu_f32(acc[nt][0]) * acc[nt][1]);
-                            z1 = f32_to_f16_bits(silu_f32(acc[nt][2]) * acc[nt][3]);
+                            z0 = f32_to_f16_rne(silu_f32(acc[nt][0]) * acc[nt][1]);
+                            z1 = f32_to_f16_rne(silu_f32(acc[nt][2]) * acc[nt][3]);
                         }
                         *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
                     } else {
-                        const float w = wts[nt];
-                        *reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q) =
-                            make_float4(w * acc[nt][0], w * acc[nt][1], w * acc[nt][2], w * acc[nt][3]);
+                        store_slot_out(a, size_t(slot) * a.R + 16 * strip + 4 * q, wts[nt], acc[nt][0], acc[nt][1],
+                                       acc[nt][2], acc[nt][3]);
                     }
                 }
 #pragma unroll

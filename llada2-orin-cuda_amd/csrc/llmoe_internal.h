@@ -132,8 +132,9 @@ __device__ __forceinline__ float silu_f32(float g) {
     return g * q;
 }
 
-// fp32 -> fp16 with round-to-nearest-even on exact ties, in integer ops. (Measured on gfx950: v_cvt_f16_f32
-// does not round every exact halfway case to even, so the hardware conversion is not used.)
+// fp32 -> fp16 with round-to-nearest-even, spelled out in integer ops: the definition the CPU checker restates
+// (orc_f32_to_f16). The kernels use the hardware conversion below; llmoe_selftest_f16 checks on the device that the
+// two agree on every finite fp32 input.
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     const uint32_t x = __float_as_uint(f);
     const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
@@ -149,6 +150,15 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     h = ax >= 0x477ff000u ? 0x7c00u : h;                                          // >= 65520 rounds to inf
     h = ax >= 0x7f800000u ? (0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u)) : h;    // inf / nan
     return uint16_t(sign | h);
+}
+
+// fp32 -> fp16, round to nearest even, by v_cvt_f16_f32 (the default rounding mode): one instruction, and the same
+// bits as f32_to_f16_bits for every finite input (an exhaustive sweep over the 2^32 patterns, llmoe_selftest_f16);
+// a NaN input gives a NaN. The fp32 value is made opaque first: otherwise the compiler folds a preceding multiply
+// into v_fma_mixlo_f16, which rounds the exact product to fp16 once instead of rounding to fp32 and then to fp16.
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+    asm("" : "+v"(f));
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
 // int32 -> fp32 through the MFMA accumulator: a product that starts from I2F_BIAS (the bits of 1.5 * 2^23) ends as
@@ -191,7 +201,7 @@ __device__ __forceinline__ uint64_t wave_incl_scan(uint64_t v) {
 
 // The gate_up output fp16(SiLU(g) u) with the hardware transcendentals (v_exp_f32, v_rcp_f32) and conversion
 // (v_cvt_f16_f32): the precision of the reference's own __expf / __fdividef / __float2half (engine/moe_i8.cu:221),
-// within the fp32-stage tolerance, not bit-identical to silu_f32 / f32_to_f16_bits.
+// within the fp32-stage tolerance, not bit-identical to silu_f32.
 __device__ __forceinline__ uint16_t silu_mul_f16_fast(float g, float u) {
     const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
     const float y = (g * __builtin_amdgcn_rcpf(1.0f + e)) * u;
@@ -334,6 +344,7 @@ struct GemmArgs {
     int R;                      // output rows (2I for gate_up, H for down)
     uint16_t* Z;                // gate_up out [slots, R/2] fp16
     float* Y;                   // down out [slots, R]
+    uint16_t* Yh;               // down, fast numerics: out as fp16 [slots, R] (round to nearest even) instead of Y
     int32_t* P;                 // group-products out [n, R, K/128] (test entry)
     const int* tstart;          // tiled: [G + 1] first task of each workgroup (the work partition above)
     int accumulate;             // GEMM_DENSE: Y += acc instead of Y = acc
@@ -345,6 +356,19 @@ struct GemmArgs {
     float* xs_out;
     int* xsum_out;
 };
+
+// The down GEMM's slot outputs w acc of one lane (4 consecutive rows from element index i): fp32 into Y, or, with
+// fast numerics, rounded to fp16 (nearest even) into Yh
+__device__ __forceinline__ void store_slot_out(const GemmArgs& a, size_t i, float w, float a0, float a1, float a2,
+                                               float a3) {
+    if (a.Yh) {
+        const uint32_t h0 = f32_to_f16_rne(w * a0) | (uint32_t(f32_to_f16_rne(w * a1)) << 16);
+        const uint32_t h1 = f32_to_f16_rne(w * a2) | (uint32_t(f32_to_f16_rne(w * a3)) << 16);
+        *reinterpret_cast<uint2*>(a.Yh + i) = make_uint2(h0, h1);
+    } else {
+        *reinterpret_cast<float4*>(a.Y + i) = make_float4(w * a0, w * a1, w * a2, w * a3);
+    }
+}
 
 // GEMM_DENSE: a plain W.A8 projection [R, 2048] (rows in packlib order), out Y[token, r] = acc (or += acc)
 enum GemmMode { GEMM_GATE_UP = 0, GEMM_DOWN = 1, GEMM_PRODUCTS_GATE_UP = 2, GEMM_PRODUCTS_DOWN = 3, GEMM_DENSE = 4 };
@@ -366,11 +390,14 @@ int tiled_grid(int mode);
 hipError_t launch_tiled_gemm(int mode, const GemmArgs& a, hipStream_t st);
 hipError_t launch_relayout(const uint8_t* src, uint8_t* dst, int R, int K, int bits, int gate_up, hipStream_t st);
 hipError_t launch_quant_a8(const float* x, int rows, int cols, int8_t* q, float* s, int* sum, hipStream_t st);
+// every finite fp32 input through f32_to_f16_rne and f32_to_f16_bits; differences counted into *mismatches
+hipError_t launch_f16_selftest(unsigned long long* mismatches, hipStream_t st);
 hipError_t launch_fwht_a8(const uint16_t* Z, int nslots, int8_t* q, float* s, int* sum, hipStream_t st);
 // combine + FWHT-2048 un-rotation + residual into h + next-layer RMSNorm / rotation / A8 (H = 2048)
-hipError_t launch_combine_norm(const float* Y, const int* tok_slots, int T, int kk, int K1, const float* signs,
-                               float eps, float* h, int8_t* q, float* s, int* sum, hipStream_t st);
-hipError_t launch_combine(const float* Y, const int* tok_slots, int T, int H, int kk, int K1, float* out,
+// (Y: fp32 [S, H], or fp16 bits when yhalf is set -- the down GEMM's fast-numerics output)
+hipError_t launch_combine_norm(const void* Y, int yhalf, const int* tok_slots, int T, int kk, int K1,
+                               const float* signs, float eps, float* h, int8_t* q, float* s, int* sum, hipStream_t st);
+hipError_t launch_combine(const void* Y, int yhalf, const int* tok_slots, int T, int H, int kk, int K1, float* out,
                           hipStream_t st);
 // router logits partials; with q != nullptr also the A8 of x (q, qs, qsum as launch_quant_a8), H = 2048
 hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, int E, float* part, int8_t* q,

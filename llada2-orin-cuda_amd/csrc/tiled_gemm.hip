@@ -418,14 +418,13 @@ __device__ __forceinline__ void rowblock_store(const GemmArgs& a, const Item& it
                         z0 = silu_mul_f16_fast(acc[s][nt][0], acc[s][nt][1]);
                         z1 = silu_mul_f16_fast(acc[s][nt][2], acc[s][nt][3]);
                     } else {
-                        z0 = f32_to_f16_bits(silu_f32(acc[s][nt][0]) * acc[s][nt][1]);
-                        z1 = f32_to_f16_bits(silu_f32(acc[s][nt][2]) * acc[s][nt][3]);
+                        z0 = f32_to_f16_rne(silu_f32(acc[s][nt][0]) * acc[s][nt][1]);
+                        z1 = f32_to_f16_rne(silu_f32(acc[s][nt][2]) * acc[s][nt][3]);
                     }
                     *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
                 } else {
-                    const float w = a.slot_weight[slot];
-                    *reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q) =
-                        make_float4(w * acc[s][nt][0], w * acc[s][nt][1], w * acc[s][nt][2], w * acc[s][nt][3]);
+                    store_slot_out(a, size_t(slot) * a.R + 16 * strip + 4 * q, a.slot_weight[slot], acc[s][nt][0],
+                                   acc[s][nt][1], acc[s][nt][2], acc[s][nt][3]);
                 }
             }
         }

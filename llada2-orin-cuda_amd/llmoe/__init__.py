@@ -66,7 +66,7 @@ EXPORTS = [
     "llmoe_experts", "llmoe_experts_norm", "llmoe_layer_forward", "llmoe_layer_buffers", "llmoe_layer_weight_bytes",
     "llmoe_group_products", "llmoe_layer_set_profiling", "llmoe_layer_stage_ms", "llmoe_layer_time_stage", "llmoe_layers_time_stage",
     "llmoe_layer_load", "llmoe_model_signs", "llmoe_dense_create", "llmoe_dense_destroy", "llmoe_dense_forward",
-    "llmoe_last_error", "llmoe_experts_scratch", "llmoe_layer_set_numerics",
+    "llmoe_last_error", "llmoe_experts_scratch", "llmoe_layer_set_numerics", "llmoe_selftest_f16",
 ]
 
 STAGES = ["quant", "router", "route", "dispatch", "gate_up", "fwht", "down", "combine"]
@@ -103,6 +103,7 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.llmoe_layer_buffers.argtypes = [vp, ctypes.POINTER(Buffers)]
     lib.llmoe_layer_weight_bytes.argtypes = [vp, ctypes.POINTER(sz)]
     lib.llmoe_group_products.argtypes = [vp, i, i, vp, vp, i, vp, vp]
+    lib.llmoe_selftest_f16.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
     lib.llmoe_layer_set_profiling.argtypes = [vp, i]
     lib.llmoe_layer_set_numerics.argtypes = [vp, i]
     lib.llmoe_layer_stage_ms.argtypes = [vp, ctypes.POINTER(ctypes.c_float)]
@@ -326,6 +327,14 @@ class Dense:
             self.close()
         except Exception:
             pass
+
+
+def selftest_f16() -> int:
+    """llmoe_selftest_f16: the number of finite fp32 inputs on which the device's hardware fp16 conversion differs
+    from round-to-nearest-even in integer ops (0 expected)."""
+    n = ctypes.c_uint64()
+    _check(load_library().llmoe_selftest_f16(ctypes.byref(n)))
+    return int(n.value)
 
 
 def time_stage_layers(layers, stage: str, reps: int = 20, stream=None) -> float:

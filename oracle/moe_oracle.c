@@ -449,7 +449,7 @@ static void free_unpacked(unpacked* u) {
 
 /* zin != NULL: the gate_up outputs Z of every slot are given (gate_up is skipped; xq, xs, xsum unused) */
 static int experts_impl(const orc_layer* L, const int8_t* xq, const float* xs, const int32_t* xsum,
-                        const uint16_t* zin, int T, const int32_t* count, const int32_t* start,
+                        const uint16_t* zin, int yhalf, int T, const int32_t* count, const int32_t* start,
                         const int32_t* slot_token, const float* slot_weight, const int32_t* tok_slots, uint16_t* Z,
                         int8_t* zq, float* zs, int32_t* zsum, float* Y, float* out, int nthreads) {
     const int H = L->H, I = L->I, E = L->E, K = L->K, GH = H / GROUP, GI = I / GROUP;
@@ -503,8 +503,11 @@ static int experts_impl(const orc_layer* L, const int8_t* xq, const float* xs, c
                 /* down: Y[slot, h] = w_slot * acc_h */
                 orc_group_products(u.d_c, u.d_z, H, I, qrow, sumrow, P);
                 const float w = slot_weight[slot];
-                for (int h = 0; h < H; ++h)
-                    Yw[(size_t)slot * H + h] = w * row_epilogue(P + (size_t)h * GI, u.d_s + (size_t)h * GI, srow, GI);
+                for (int h = 0; h < H; ++h) {
+                    const float y = w * row_epilogue(P + (size_t)h * GI, u.d_s + (size_t)h * GI, srow, GI);
+                    /* yhalf: the build's fast-numerics slot outputs, rounded to fp16 (nearest even) */
+                    Yw[(size_t)slot * H + h] = yhalf ? orc_f16_to_f32(orc_f32_to_f16(y)) : y;
+                }
             }
         }
         free(P); free(perm); free(gacc);
@@ -528,14 +531,15 @@ int orc_experts(const orc_layer* L, const int8_t* xq, const float* xs, const int
                 const int32_t* count, const int32_t* start, const int32_t* slot_token, const float* slot_weight,
                 const int32_t* tok_slots, uint16_t* Z, int8_t* zq, float* zs, int32_t* zsum, float* Y, float* out,
                 int nthreads) {
-    return experts_impl(L, xq, xs, xsum, NULL, T, count, start, slot_token, slot_weight, tok_slots, Z, zq, zs, zsum, Y,
+    return experts_impl(L, xq, xs, xsum, NULL, 0, T, count, start, slot_token, slot_weight, tok_slots, Z, zq, zs, zsum, Y,
                         out, nthreads);
 }
 
-int orc_experts_from_z(const orc_layer* L, const uint16_t* Z, int T, const int32_t* count, const int32_t* start,
-                       const int32_t* slot_token, const float* slot_weight, const int32_t* tok_slots, int8_t* zq,
-                       float* zs, int32_t* zsum, float* Y, float* out, int nthreads) {
-    return experts_impl(L, NULL, NULL, NULL, Z, T, count, start, slot_token, slot_weight, tok_slots, NULL, zq, zs,
+int orc_experts_from_z(const orc_layer* L, const uint16_t* Z, int yhalf, int T, const int32_t* count,
+                       const int32_t* start, const int32_t* slot_token, const float* slot_weight,
+                       const int32_t* tok_slots, int8_t* zq, float* zs, int32_t* zsum, float* Y, float* out,
+                       int nthreads) {
+    return experts_impl(L, NULL, NULL, NULL, Z, yhalf, T, count, start, slot_token, slot_weight, tok_slots, NULL, zq, zs,
                         zsum, Y, out, nthreads);
 }
 

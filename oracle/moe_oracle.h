@@ -73,10 +73,13 @@ int orc_experts(const orc_layer* L, const int8_t* xq, const float* xs, const int
                 const int32_t* tok_slots, uint16_t* Z, int8_t* zq, float* zs, int32_t* zsum, float* Y, float* out,
                 int nthreads);
 
-/* orc_experts from the gate_up outputs Z [S, I] (fp16 bits) of every slot: FWHT-512 + A8, down, combine. */
-int orc_experts_from_z(const orc_layer* L, const uint16_t* Z, int T, const int32_t* count, const int32_t* start,
-                       const int32_t* slot_token, const float* slot_weight, const int32_t* tok_slots, int8_t* zq,
-                       float* zs, int32_t* zsum, float* Y, float* out, int nthreads);
+/* orc_experts from the gate_up outputs Z [S, I] (fp16 bits) of every slot: FWHT-512 + A8, down, combine. yhalf != 0:
+ * each slot output is rounded to fp16 (nearest even) before the combine -- the build's fast-numerics Y -- and Y
+ * returns those values as fp32. */
+int orc_experts_from_z(const orc_layer* L, const uint16_t* Z, int yhalf, int T, const int32_t* count,
+                       const int32_t* start, const int32_t* slot_token, const float* slot_weight,
+                       const int32_t* tok_slots, int8_t* zq, float* zs, int32_t* zsum, float* Y, float* out,
+                       int nthreads);
 
 /* Independent fp64 dequantize-then-matmul reference (engine/tests/gen_moe_case.py:77-93): acc[t] =
  * sum_k w_k * d(a8(fp16(SiLU(g x') * (u x')) H512)) with x' = a8(x) dequantised, plus the shared expert

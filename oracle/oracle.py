@@ -49,7 +49,7 @@ def lib() -> ctypes.CDLL:
         L.orc_experts.argtypes = [ctypes.POINTER(OrcLayer), vp, vp, vp, i, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
                                   vp, i]
         L.orc_experts.restype = i
-        L.orc_experts_from_z.argtypes = [ctypes.POINTER(OrcLayer), vp, i, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i]
+        L.orc_experts_from_z.argtypes = [ctypes.POINTER(OrcLayer), vp, i, i, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i]
         L.orc_experts_from_z.restype = i
         L.orc_reference_f64.argtypes = [ctypes.POINTER(OrcLayer), vp, i, vp, vp, vp, i]
         L.orc_reference_f64.restype = i
@@ -234,8 +234,10 @@ class Layer:
             raise RuntimeError(f"orc_experts failed: {rc}")
         return dict(out=out, Y=Y, Z=Z, zq=zq, zs=zs, zsum=zsum, **dsp)
 
-    def experts_from_z(self, Z, topk, topw, nthreads=0):
-        """The expert stage after gate_up, from given fp16 Z [S, I] bits: FWHT-512 + A8, down, combine."""
+    def experts_from_z(self, Z, topk, topw, nthreads=0, y_half=False):
+        """The expert stage after gate_up, from given fp16 Z [S, I] bits: FWHT-512 + A8, down, combine. y_half: the
+        slot outputs Y rounded to fp16 (nearest even) before the combine, as the build's fast numerics store them
+        (Y is returned as fp32 holding those fp16 values)."""
         L = self.layer
         H, I, E = L["H"], L["I"], L["E"]
         T = topk.shape[0]
@@ -247,7 +249,7 @@ class Layer:
         zsum = np.zeros((S, 4), np.int32)
         Y = np.zeros((S, H), np.float32)
         out = np.zeros((T, H), np.float32)
-        rc = lib().orc_experts_from_z(ctypes.byref(self.c), _p(Z), T, _p(dsp["count"]), _p(dsp["start"]),
+        rc = lib().orc_experts_from_z(ctypes.byref(self.c), _p(Z), int(y_half), T, _p(dsp["count"]), _p(dsp["start"]),
                                       _p(dsp["slot_token"]), _p(dsp["slot_weight"]), _p(dsp["tok_slots"]), _p(zq),
                                       _p(zs), _p(zsum), _p(Y), _p(out), nthreads)
         if rc != 0:

@@ -80,6 +80,14 @@ def test_quant_a8_bit_exact(gpu, rows):
     assert np.array_equal(sm.cpu().numpy(), sum_ref)
 
 
+def test_hw_f16_conversion_is_round_to_nearest_even(gpu):
+    """The kernels round fp32 -> fp16 with v_cvt_f16_f32; the CPU checker restates round-to-nearest-even in integer
+    ops (pinned against numpy in the CPU suite). Every finite fp32 bit pattern gives the same bits both ways."""
+    import llmoe
+    say("[f16 self-test] all 2^32 patterns")
+    assert llmoe.selftest_f16() == 0
+
+
 @pytest.mark.parametrize("bits", [2, 3, 4, 8])
 @pytest.mark.parametrize("which", [0, 1])
 def test_group_products_bit_exact(gpu, bits, which):

@@ -371,3 +371,20 @@ def test_experts_from_z_reproduces_the_expert_stage():
     rz = O.Layer(layer).experts_from_z(r["Z"], r["topk"], r["topw"])
     for k in ("zq", "zs", "zsum", "Y", "out"):
         np.testing.assert_array_equal(np.asarray(rz[k]).view(np.uint8), np.asarray(r[k]).view(np.uint8), err_msg=k)
+
+
+def test_experts_from_z_half_slot_outputs():
+    """y_half: the slot outputs are the exact ones rounded to fp16 (numpy's round to nearest even) and the combine is
+    the fixed-order fp32 sum of those; the output stays within the contract's 1e-3 of the exact one."""
+    layer = synth.make_layer(8, E=64, mix="mixed", shared=True)
+    x = synth.make_x(3, 8)
+    r = O.Layer(layer).forward(x, C=64)
+    rh = O.Layer(layer).experts_from_z(r["Z"], r["topk"], r["topw"], y_half=True)
+    np.testing.assert_array_equal(rh["Y"].view(np.uint32),
+                                  r["Y"].astype(np.float16).astype(np.float32).view(np.uint32))
+    acc = np.zeros_like(rh["out"])
+    for k in range(9):
+        acc = acc + rh["Y"][r["tok_slots"][:, k]]
+    np.testing.assert_array_equal(acc.view(np.uint32), rh["out"].view(np.uint32))
+    err = np.abs(rh["out"] - r["out"]).max() / np.abs(r["out"]).max()
+    assert 0 < err <= 1e-3, err
