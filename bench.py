@@ -149,9 +149,15 @@ def norm_step(llmoe, torch, Gs, x, steps, warmup):
             "combine_ms": llmoe.time_stage_layers(Gs, "combine", 20)}
 
 
+FAST = True   # measure each configuration in LLMOE_NUMERICS_FAST as well (--no-fast: exact mode only)
+
+
 def fast_numerics(llmoe, Gs, fn, steps, warmup, tokens, layers_per_step=1):
-    """The same step with LLMOE_NUMERICS_FAST (the gate_up SiLU by the hardware transcendentals): step time and the
-    steady-state gate_up duration; the layers are left in exact mode."""
+    """The same step with LLMOE_NUMERICS_FAST (the gate_up SiLU by the hardware transcendentals; fp16 slot outputs
+    for several routing blocks): step time and the steady-state gate_up duration; the layers are left in exact
+    mode. None when FAST is off."""
+    if not FAST:
+        return None
     for G in Gs:
         G.set_numerics(True)
     dt = time_steps(fn, steps, warmup)
@@ -427,7 +433,10 @@ def main():
     ap.add_argument("--only", choices=["config2", "config4-2", "config4-4", "config4-8"],
                     help="one prefill configuration only, printed as its own JSON line (profiling runs)")
     ap.add_argument("--copy-calibration", action="store_true", help="run 512 MiB device copies first (counter runs)")
+    ap.add_argument("--no-fast", action="store_true", help="exact numerics only (profiling runs of one kernel variant)")
     args = ap.parse_args()
+    global FAST
+    FAST = not args.no_fast
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (expert parallelism is a design note "
               "only); run with --gpus 1", file=sys.stderr)
