@@ -80,6 +80,24 @@ def test_quant_a8_bit_exact(gpu, rows):
     assert np.array_equal(sm.cpu().numpy(), sum_ref)
 
 
+def test_fwht_stage_fused_at_decode(gpu):
+    """One routing block: FWHT-512 + A8 runs inside the streamed down GEMM, so re-launching the FWHT stage alone is
+    refused (its time is in the down stage); with several blocks the standalone FWHT kernel re-launches."""
+    import torch
+    import llmoe
+    say("[fwht stage] T=32 and T=64")
+    L = layer_for("mixed", True)
+    G = make_gpu_layer(L, 256)
+    run_layer(G, synth.make_x(70, 32), gpu)
+    with pytest.raises(llmoe.LLMoEError, match="fused into the down GEMM"):
+        G.time_stage("fwht", reps=2)
+    assert G.time_stage("down", reps=2) > 0
+    run_layer(G, synth.make_x(71, 64), gpu)
+    assert G.time_stage("fwht", reps=2) > 0
+    torch.cuda.synchronize()
+    G.close()
+
+
 def test_hw_f16_conversion_is_round_to_nearest_even(gpu):
     """The kernels round fp32 -> fp16 with v_cvt_f16_f32; the CPU checker restates round-to-nearest-even in integer
     ops (pinned against numpy in the CPU suite). Every finite fp32 bit pattern gives the same bits both ways."""
