@@ -41,19 +41,27 @@ __global__ void __launch_bounds__(256) fwht_a8_kernel(const uint16_t* __restrict
 
 // out[t, :] = sum_{k < kk} Y[tok_slots[t, k], :], k ascending (engine/moe_i8.cu:505-515). grid (T, column slices).
 constexpr int MAX_KK = 9;   // top-8 + the shared expert
-// 4 consecutive slot outputs from element index i of Y: fp32, or fp16 bits (HALF, the fast-numerics down output)
-template <bool HALF>
+// 4 consecutive slot outputs from element index i of Y: fp32, or fp16 bits (HALF, the fast-numerics down output).
+// STREAM: non-temporal loads, for an fp32 Y far larger than the caches (more than 256 tokens: the combine then
+// reads 5-8 % faster), not for a decode step's Y, which is still in the caches (there they cost 1.5 us), nor for
+// fp16 rows (measured 6-35 % slower).
+template <bool HALF, bool STREAM = false>
 __device__ __forceinline__ float4 load_y4(const void* __restrict__ Y, size_t i) {
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    typedef unsigned int v2u __attribute__((ext_vector_type(2)));
     if constexpr (HALF) {
-        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(Y) + i);
+        const v2u* p = reinterpret_cast<const v2u*>(static_cast<const uint16_t*>(Y) + i);
+        const v2u u = STREAM ? __builtin_nontemporal_load(p) : *p;
         return make_float4(f16_bits_to_f32(u.x & 0xFFFFu), f16_bits_to_f32(u.x >> 16), f16_bits_to_f32(u.y & 0xFFFFu),
                            f16_bits_to_f32(u.y >> 16));
     } else {
-        return *reinterpret_cast<const float4*>(static_cast<const float*>(Y) + i);
+        const v4f* p = reinterpret_cast<const v4f*>(static_cast<const float*>(Y) + i);
+        const v4f v = STREAM ? __builtin_nontemporal_load(p) : *p;
+        return make_float4(v.x, v.y, v.z, v.w);
     }
 }
 
-template <bool HALF>
+template <bool HALF, bool STREAM>
 __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ Y, const int* __restrict__ tok_slots,
                                                       int H, int kk, int K1, float* __restrict__ out) {
     const int t = blockIdx.x;
@@ -71,7 +79,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ Y
             const int h = hb + r * blockDim.x * 4;
 #pragma unroll
             for (int k = 0; k < MAX_KK; ++k)
-                if (k < kk && h < h1) v[r][k] = load_y4<HALF>(Y, size_t(sl[k]) * H + h);
+                if (k < kk && h < h1) v[r][k] = load_y4<HALF, STREAM>(Y, size_t(sl[k]) * H + h);
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -273,9 +281,13 @@ hipError_t launch_combine(const void* Y, int yhalf, const int* tok_slots, int T,
     // a decode step's few rows are split over 8 column slices (256 columns, one pass of 64 threads x 2 float4)
     const int ns = T <= 256 && H % 256 == 0 ? H / 256 : 1;
     const dim3 grid(T, ns);
-    const int nth = ns > 1 ? 64 : 256;
-    if (yhalf) combine_kernel<true><<<grid, nth, 0, st>>>(Y, tok_slots, H, kk, K1, out);
-    else combine_kernel<false><<<grid, nth, 0, st>>>(Y, tok_slots, H, kk, K1, out);
+    if (ns > 1) {
+        if (yhalf) combine_kernel<true, false><<<grid, 64, 0, st>>>(Y, tok_slots, H, kk, K1, out);
+        else combine_kernel<false, false><<<grid, 64, 0, st>>>(Y, tok_slots, H, kk, K1, out);
+    } else {   // more than 256 tokens: an fp32 Y (>= 18 MB) streams through (fp16 rows measured slower that way)
+        if (yhalf) combine_kernel<true, false><<<grid, 256, 0, st>>>(Y, tok_slots, H, kk, K1, out);
+        else combine_kernel<false, true><<<grid, 256, 0, st>>>(Y, tok_slots, H, kk, K1, out);
+    }
     return hipGetLastError();
 }
 
