@@ -167,16 +167,27 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, con
     int* bsum = reinterpret_cast<int*>(bs + G * NTOK);
     const int ntok = it.ntok;
     if (MODE == GEMM_DOWN && a.zin != nullptr) {
-        // B rows = A8(FWHT-512(Z)) of the item's slots, one wave per slot (the operations of fwht_a8_kernel); the
-        // units of row block 0 also store them for the buffers' readers. Rows n >= ntok are zero.
-#pragma unroll 1
-        for (int n = wave; n < NTOK; n += WAVES) {
+        // B rows = A8(FWHT-512(Z)) of the item's slots, slot n on wave n % WAVES (the operations of
+        // fwht_a8_kernel); the units of row block 0 also store them for the buffers' readers. Rows n >= ntok are
+        // zero. The wave's Z rows are all loaded before the first transform, so their latencies overlap.
+        constexpr int PERW = NTOK / WAVES;
+        static_assert(PERW * WAVES == NTOK, "slots per wave");
+        uint4 zraw[PERW];
+#pragma unroll
+        for (int i = 0; i < PERW; ++i) {
+            const int n = wave + i * WAVES;
+            zraw[i] = n < ntok ? *reinterpret_cast<const uint4*>(a.zin + size_t(it.slot0 + n) * K + 8 * lane)
+                               : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int i = 0; i < PERW; ++i) {
+            const int n = wave + i * WAVES;
             uint2 qw = make_uint2(0u, 0u);
             float sc = 0.0f;
             int tot = 0;
             if (n < ntok) {
                 const size_t slot = size_t(it.slot0 + n);
-                fwht512_a8(a.zin + slot * K, lane, qw, sc, tot);
+                fwht512_a8_raw(zraw[i], lane, qw, sc, tot);
                 if (row_block == 0) {
                     *reinterpret_cast<uint2*>(a.xq_out + slot * K + 8 * lane) = qw;
                     if ((lane & 15) == 0) {

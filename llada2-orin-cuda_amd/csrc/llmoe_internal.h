@@ -234,8 +234,8 @@ __device__ __forceinline__ int clamp127(float r) { return int(fminf(fmaxf(r, -12
 // values 8l .. 8l+7; butterfly stages h = 1, 2, 4 in registers, h = 8 .. 256 by lane shuffles (xor 1 .. 32), in
 // ascending h; the group quantiser multiplies by 1/s. Out (logical order): the lane's 8 codes, and its group's
 // scale and code sum (group = lane / 16). All 64 lanes must be active.
-__device__ __forceinline__ void fwht512_a8(const uint16_t* __restrict__ zrow, int lane, uint2& qw, float& sc, int& tot) {
-    const uint4 raw = *reinterpret_cast<const uint4*>(zrow + 8 * lane);
+// fwht512_a8_raw: the same from the lane's 16 bytes of the row, already loaded (raw = the row's bytes 16l .. 16l+15).
+__device__ __forceinline__ void fwht512_a8_raw(const uint4& raw, int lane, uint2& qw, float& sc, int& tot) {
     const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
     float x[8];
 #pragma unroll
@@ -280,6 +280,9 @@ __device__ __forceinline__ void fwht512_a8(const uint16_t* __restrict__ zrow, in
     }
     qw = make_uint2(w0, w1);
     tot = group16_sum(t);
+}
+__device__ __forceinline__ void fwht512_a8(const uint16_t* __restrict__ zrow, int lane, uint2& qw, float& sc, int& tot) {
+    fwht512_a8_raw(*reinterpret_cast<const uint4*>(zrow + 8 * lane), lane, qw, sc, tot);
 }
 
 // A8 of 512 consecutive values by one wave (engine/ops.cu:42-66): lane l owns values 8l .. 8l+7, a 128-group is
