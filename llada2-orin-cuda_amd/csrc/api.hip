@@ -13,7 +13,7 @@
 #include <vector>
 
 #include "llmoe.h"
-#include "llmoe_internal.h"
+#include "decode_plan.h"
 
 using namespace llmoe;
 
@@ -113,6 +113,9 @@ struct llmoe_layer {
     // routing state
     int routed_T = -1, ntok = 16, max_items = 0;
     bool tiled = false;                             // the routing of routed_T may have tiled units
+    // a layer forward's decode routing left its masks for the gate_up GEMM to plan from (no dispatch kernel ran):
+    // the next expert call plans in its gate_up GEMM and its down GEMM zeroes the masks
+    bool plan_pending = false;
     // stage timing
     bool profiling = false;
     hipEvent_t ev[2 * LLMOE_N_STAGES] = {};
@@ -410,9 +413,13 @@ namespace {
 // routing; with quant set (and x given) the router kernel also writes the A8 of x into the layer workspace; with
 // xa8 set (routing from logits) the first per-token routing kernel writes the A8 of xa8 there
 int route_impl(llmoe_layer* L, const float* x, const float* logits, int T, hipStream_t st, bool quant,
-               const float* xa8 = nullptr) {
+               const float* xa8 = nullptr, bool defer_dispatch = false) {
     const auto& d = L->d;
     L->routed_T = -1;
+    if (L->plan_pending) {   // a forward's routing masks that no expert call consumed
+        L->plan_pending = false;
+        HIPCHECK(launch_zero_decode_state(L->blockmax, L->tmask, d.n_experts, st));
+    }
     if (int rc = prepare_items(L, T)) return rc;
     const float* part = logits;
     int nchunks = 1;
@@ -431,9 +438,10 @@ int route_impl(llmoe_layer* L, const float* x, const float* logits, int T, hipSt
         HIPCHECK(launch_decode_route(part, nchunks, L->bias, T, d.n_experts, d.top_k, d.pool, d.routed_scale, L->sig,
                                      L->topk, L->topw, L->blockmax, L->tmask, d.has_shared, L->bits_d,
                                      L->count, L->start, L->units_gu, L->units_dn, L->n_units, L->slot_token,
-                                     L->slot_weight, L->tok_slots, qx, st));
+                                     L->slot_weight, L->tok_slots, qx, defer_dispatch ? 0 : 1, st));
         L->mark(LLMOE_STAGE_ROUTE, true, st);
         L->routed_T = T;
+        L->plan_pending = defer_dispatch;
         return LLMOE_OK;
     }
     HIPCHECK(launch_route(part, nchunks, L->bias, T, d.n_experts, d.top_k, d.pool, d.block, d.routed_scale, L->sig,
@@ -495,8 +503,19 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     tg.n_items = L->n_units + 2;
     L->last_gu = g;
     L->last_tgu = tg;
+    // a forward's decode step: the gate_up GEMM builds the slot plan from the routing masks and writes the lists
+    // that the dispatch kernel would have (re-launches for stage timing then read those lists)
+    const bool plan = L->plan_pending && !L->tiled;
+    L->plan_pending = false;
     L->mark(LLMOE_STAGE_GATE_UP, false, st);
-    HIPCHECK(launch_gemm(GEMM_GATE_UP, g, tg, L->tiled, st));
+    if (plan) {
+        const DecodePlanArgs pa{T, d.n_experts, K, L->tmask, L->topk, L->topw,
+                                DispatchOut{d.has_shared, 16, L->bits_d, L->count, L->start, L->units_gu, L->units_dn,
+                                            L->n_units, L->slot_token, L->slot_weight, L->tok_slots}};
+        HIPCHECK(launch_expert_gemm_plan(g, pa, st));
+    } else {
+        HIPCHECK(launch_gemm(GEMM_GATE_UP, g, tg, L->tiled, st));
+    }
     L->mark(LLMOE_STAGE_GATE_UP, true, st);
     L->mark(LLMOE_STAGE_FWHT, false, st);
     // FWHT-512 + A8 of Z: its own kernel before the tiled down GEMM; the streamed down GEMM stages it per item
@@ -517,6 +536,11 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     g.fast = 0;
     tg = g;
     g.zin = w.Z; g.xq_out = w.zq; g.xs_out = w.zs; g.xsum_out = w.zsum;
+    if (plan) {
+        g.clear_a = L->tmask;
+        g.clear_b = L->blockmax;
+        g.nclear = d.n_experts;
+    }
     tg.items = L->tunits_dn;
     tg.tstart = L->tstart + L->g_gu + 1;
     tg.n_items = L->n_units + 3;
@@ -589,7 +613,9 @@ int llmoe_layer_forward(llmoe_layer* L, const float* x, const float* logits, int
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (!logits && !L->router_w) return fail(LLMOE_EINVAL, "layer created without a router matrix");
     // the A8 of x rides on the first routing kernel: the router's (x·Wr) or, from given logits, the per-token one
-    if (int rc = route_impl(L, logits ? nullptr : x, logits, T, st, logits == nullptr, logits ? x : nullptr)) return rc;
+    // at decode the dispatch is left to the gate_up GEMM (plan_pending)
+    if (int rc = route_impl(L, logits ? nullptr : x, logits, T, st, logits == nullptr, logits ? x : nullptr, true))
+        return rc;
     return llmoe_experts(L, L->xq, L->xs, L->xsum, T, out, stream);
 }
 

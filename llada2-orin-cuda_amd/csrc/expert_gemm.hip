@@ -18,7 +18,7 @@
 //   products (MODE 2, 3): raw P_g per (token, row, group) in either geometry, for the bit-exactness test.
 #include <type_traits>
 
-#include "llmoe_internal.h"
+#include "decode_plan.h"
 
 namespace llmoe {
 
@@ -133,9 +133,15 @@ __host__ __device__ constexpr int lds_bytes() {
     return b_bytes(16 * NT, Geo<MODE>::NSB * SB_K) + meta_bytes<MODE>() + 16 * NT * 4;   // + the B row table
 }
 
-template <int BITS, int MODE, int NT>
+// the plan of a self-planning decode gate_up GEMM: the unit's token rows come from its token masks
+struct RowSrc {
+    const DecodePlan* P;
+    int T, K, E;
+};
+
+template <int BITS, int MODE, int NT, bool PLAN = false>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, const uint8_t* mat_e, uint8_t* lds,
-                                          int row_block) {
+                                          int row_block, const RowSrc& rs = RowSrc{}) {
     constexpr int NSB = Geo<MODE>::NSB, SPW = Geo<MODE>::template spw<BITS>(), NSTEP = NSB * SPW;
     constexpr int D = Ring<BITS>::D < NSTEP ? Ring<BITS>::D : NSTEP;
     static_assert(NSTEP % 4 == 0 && 4 % D == 0, "ring geometry");
@@ -207,8 +213,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, con
         // bytes over 256 threads at clamped rows, all issued before the LDS stores
         int* rowtab = reinterpret_cast<int*>(meta_lds + meta_bytes<MODE>());
         if (threadIdx.x < NTOK) {
-            const int slot = it.slot0 + min(int(threadIdx.x), ntok - 1);
-            rowtab[threadIdx.x] = a.slot_token ? a.slot_token[slot] : slot;
+            const int n = min(int(threadIdx.x), ntok - 1), slot = it.slot0 + n;
+            if constexpr (PLAN) rowtab[threadIdx.x] = decode_slot_token(*rs.P, it, n, rs.T, rs.K, rs.E);
+            else rowtab[threadIdx.x] = a.slot_token ? a.slot_token[slot] : slot;
         }
         __syncthreads();
         constexpr int CH = K / 16, PER = (NTOK * CH + WAVES * 64 - 1) / (WAVES * 64);
@@ -422,6 +429,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, con
 template <int MODE, int NT>
 __global__ void __launch_bounds__(WAVES * 64, NT == 1 ? 3 : 1) expert_gemm(GemmArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
+    if (MODE == GEMM_DOWN && a.clear_a != nullptr && blockIdx.x == 0)
+        for (int i = threadIdx.x; i < a.nclear; i += blockDim.x) {
+            a.clear_a[i] = 0u;
+            a.clear_b[i] = 0u;
+        }
     // the unit and the expert's code width and matrix offset are read through the scalar cache (constant address
     // space: the lists are written by earlier kernels only), the width and offset together, so the weight stream
     // starts after two short dependent loads
@@ -438,6 +450,37 @@ __global__ void __launch_bounds__(WAVES * 64, NT == 1 ? 3 : 1) expert_gemm(GemmA
         else if (bits == 3) gemm_body<3, MODE, NT>(a, it, mat_e, lds, it.rb);
         else if (bits == 4) gemm_body<4, MODE, NT>(a, it, mat_e, lds, it.rb);
         else gemm_body<8, MODE, NT>(a, it, mat_e, lds, it.rb);
+        __syncthreads();   // the next unit re-stages the LDS
+    }
+}
+
+// The decode gate_up GEMM of a layer forward, planning for itself: every workgroup builds the slot plan in LDS from
+// the routing masks (decode_plan.h) and takes the units blockIdx.x, blockIdx.x + gridDim.x, ... of the gate_up list
+// that the dispatch kernel would have written; workgroups 0 .. E write the plan's lists first (expert r's units, or
+// the shared units and the placement), for the down GEMM, the combine and the buffers' readers. The routing masks
+// stay as they are (the down GEMM zeroes them).
+__global__ void __launch_bounds__(WAVES * 64, 3) expert_gemm_plan(GemmArgs a, DecodePlanArgs p) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ DecodePlan P;
+    decode_plan_scan(p.E, p.tmask, p.d.bits, P);
+    const int sbits = p.d.has_shared ? p.d.bits[p.E] : 8;
+    for (int r = blockIdx.x; r <= p.E; r += gridDim.x) {
+        if (r < p.E) decode_plan_write_expert(P, r, threadIdx.x, blockDim.x, p.d);
+        else decode_plan_write_rest(P, threadIdx.x, blockDim.x, p.T, p.E, p.K, p.topk, p.topw, p.d);
+    }
+    const int n = decode_plan_units(P, false, p.T, p.d.has_shared, sbits);
+    const RowSrc rs{&P, p.T, p.K, p.E};
+    for (int u = blockIdx.x; u < n; u += gridDim.x) {
+        const Item q = decode_plan_unit(P, false, u, p.T, p.E, p.K, sbits);
+        const Item it{__builtin_amdgcn_readfirstlane(q.expert), __builtin_amdgcn_readfirstlane(q.slot0),
+                      __builtin_amdgcn_readfirstlane(q.ntok), __builtin_amdgcn_readfirstlane(q.rb)};
+        const uint64_t off = *const_ptr(a.off + it.expert);
+        const int bits = it.expert < p.E ? __builtin_amdgcn_readfirstlane(int(P.bits[it.expert])) : sbits;
+        const uint8_t* mat_e = a.base + off;
+        if (bits == 2) gemm_body<2, GEMM_GATE_UP, 1, true>(a, it, mat_e, lds, it.rb, rs);
+        else if (bits == 3) gemm_body<3, GEMM_GATE_UP, 1, true>(a, it, mat_e, lds, it.rb, rs);
+        else if (bits == 4) gemm_body<4, GEMM_GATE_UP, 1, true>(a, it, mat_e, lds, it.rb, rs);
+        else gemm_body<8, GEMM_GATE_UP, 1, true>(a, it, mat_e, lds, it.rb, rs);
         __syncthreads();   // the next unit re-stages the LDS
     }
 }
@@ -472,12 +515,32 @@ hipError_t launch_t(const GemmArgs& a, int, hipStream_t st) {
 
 hipError_t gemm_setup() {
     hipError_t e;
+    if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(&expert_gemm_plan),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes<GEMM_GATE_UP, 1>())) != hipSuccess)
+        return e;
     if ((e = set_attr<GEMM_GATE_UP, 1>()) != hipSuccess) return e;
     if ((e = set_attr<GEMM_DOWN, 1>()) != hipSuccess) return e;
     if ((e = set_attr<GEMM_DENSE, 1>()) != hipSuccess) return e;
     if ((e = set_attr<GEMM_PRODUCTS_GATE_UP, 4>()) != hipSuccess) return e;
     if ((e = set_attr<GEMM_PRODUCTS_DOWN, 4>()) != hipSuccess) return e;
     return hipSuccess;
+}
+
+hipError_t launch_expert_gemm_plan(const GemmArgs& a, const DecodePlanArgs& p, hipStream_t st) {
+    if (p.T < 1 || p.T > 32 || p.E < 1 || p.E > PLAN_MAXE) return hipErrorInvalidValue;
+    static int grid = 0;
+    if (!grid) {   // workgroups resident at once on the whole GPU
+        int dev = 0, cus = 0, per_cu = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e == hipSuccess)
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&expert_gemm_plan),
+                                                             WAVES * 64, lds_bytes<GEMM_GATE_UP, 1>());
+        if (e != hipSuccess) return e;
+        grid = cus * (per_cu > 0 ? per_cu : 1);
+    }
+    expert_gemm_plan<<<grid, WAVES * 64, lds_bytes<GEMM_GATE_UP, 1>(), st>>>(a, p);
+    return hipGetLastError();
 }
 
 // mode: GemmMode; nt: 16-token tiles per work item, 1 for the layer GEMMs (experts with many tokens take the

@@ -358,6 +358,11 @@ struct GemmArgs {
     int8_t* xq_out;
     float* xs_out;
     int* xsum_out;
+    // streamed down GEMM after a self-planned gate_up: workgroup 0 zeroes clear_a / clear_b [nclear] (the decode
+    // routing state that the gate_up GEMM read)
+    uint32_t* clear_a;
+    uint32_t* clear_b;
+    int nclear;
 };
 
 // The down GEMM's slot outputs w acc of one lane (4 consecutive rows from element index i): fp32 into Y, or, with
@@ -386,6 +391,10 @@ size_t packlib_matrix_bytes(int R, int K, int bits);
 
 hipError_t gemm_setup();   // function attributes (dynamic LDS), once per process
 hipError_t launch_expert_gemm(int mode, int nt, const GemmArgs& a, int max_items, hipStream_t st);
+// the decode gate_up GEMM that builds the slot plan itself from the routing masks (a.items / a.n_items unused), and
+// writes the plan's lists (DecodePlanArgs::d) for the down GEMM and the combine
+struct DecodePlanArgs;
+hipError_t launch_expert_gemm_plan(const GemmArgs& a, const DecodePlanArgs& p, hipStream_t st);
 // tiled units (a.items / a.n_items): mode GEMM_GATE_UP or GEMM_DOWN
 hipError_t tiled_setup();
 // resident workgroups of the tiled GEMM grid for mode GEMM_GATE_UP / GEMM_DOWN (the G of the work partition)
@@ -409,13 +418,16 @@ hipError_t launch_route(const float* part, int nchunks, const float* bias, int T
                         float rscale, float* sig, uint32_t* blockmax, int32_t* topk, float* topw, uint32_t* mask,
                         const QuantX& qx, hipStream_t st);
 // decode step (T <= 32, one routing block): [scores and pool keys (pool < E)], selection in ceil(T/8)
-// workgroups, then one workgroup builds the slots and work units (streamed, 16 slots per item). blockmax / tmask
-// [E] must be zero on entry and are zero again on exit. sig: [T, E] scratch.
+// workgroups, then (dispatch != 0) one workgroup builds the slots and work units (streamed, 16 slots per item).
+// blockmax / tmask [E] must be zero on entry and are zero again on exit when dispatch is set; otherwise the gate_up
+// GEMM plans from them (launch_expert_gemm_plan) and the down GEMM clears them. sig: [T, E] scratch.
 hipError_t launch_decode_route(const float* part, int nchunks, const float* bias, int T, int E, int K, int C,
                                float rscale, float* sig, int32_t* topk, float* topw, uint32_t* blockmax,
                                uint32_t* tmask, int has_shared, const int8_t* bits, int32_t* count, int32_t* start,
                                Item* units_gu, Item* units_dn, int* n_units, int32_t* slot_token, float* slot_weight,
-                               int32_t* tok_slots, const QuantX& qx, hipStream_t st);
+                               int32_t* tok_slots, const QuantX& qx, int dispatch, hipStream_t st);
+// zero the decode routing state (blockmax, tmask [E]) when no kernel of the step consumed it
+hipError_t launch_zero_decode_state(uint32_t* blockmax, uint32_t* tmask, int E, hipStream_t st);
 hipError_t launch_masks(const int32_t* topk, int T, int E, int K, int block, uint32_t* mask, hipStream_t st);
 // work units: streamed units_gu / units_dn (n_units[0] / [1], items of <= ntok slots); when `tiled` is set, the
 // chunks of the experts with more than TILED_MIN slots in tunits_gu / tunits_dn (n_units[2] / [3], Item.rb =

@@ -1,7 +1,7 @@
 // Router and dispatch kernels (engine/ops.cu:137-423): router logits, per-block sigmoid+bias scoring with the
 // block expert pool and per-token top-K, routing weights, and the deterministic counting sort of (token, k)
 // pairs into expert-major slots with the GEMM work items. All counts stay on the device.
-#include "llmoe_internal.h"
+#include "decode_plan.h"
 
 namespace llmoe {
 
@@ -140,7 +140,6 @@ __device__ __forceinline__ int width_class(int bits) { return bits == 8 ? 0 : bi
 // decode units, longest first: a streamed unit's time is set by its vector work, and the 2-bit units (4 strips per
 // wave) have the most tiles (measured at 32 tokens against the byte order 8, 4, 3, 2 with the shared expert first:
 // 0.0623 -> 0.0615 ms per step)
-__device__ __forceinline__ int decode_class(int bits) { return bits == 2 ? 0 : bits == 3 ? 1 : bits == 4 ? 2 : 3; }
 
 // the units of expert e: items of <= ntok of its c slots starting at slot st, each split into row blocks
 __device__ void emit_units(int e, int c, int st, int ntok, int bits, int base_gu, int base_dn, Item* units_gu,
@@ -194,24 +193,7 @@ __device__ __forceinline__ long long floor_div(long long x, long long d) {
     return q;
 }
 
-struct DispatchOut {         // written by the single-block fused route (decode): the plan + place results
-    int has_shared, ntok;
-    const int8_t* bits;      // code width per expert [E + 1] (orders and splits the work units)
-    int* count;
-    int* start;
-    Item* units_gu;
-    Item* units_dn;
-    int* n_units;
-    int* slot_token;
-    float* slot_weight;
-    int* tok_slots;
-};
 
-// shared-expert unit u of a list with r row blocks per item (items of 16 slots at T K + 16 j)
-__device__ __forceinline__ void units_shared(Item* list, int u, int r, int E, int T, int K) {
-    const int j = u / r;
-    list[u] = Item{E, T * K + 16 * j, min(16, T - 16 * j), u % r};
-}
 
 // Descending bitonic sort of one key per lane across the 64 lanes of a wave: lane i ends with the i-th largest.
 __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t k, int lane) {
@@ -232,8 +214,8 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t k, int lane) {
 
 // ---- decode routing (one routing block, T <= block <= 32) ------------------------------------------------------
 // score_kernel (with the pool), select_token_kernel (one token per workgroup), then dispatch_kernel (one
-// workgroup: slots and work units for all tokens). DecodeState is zero when a call starts, and dispatch_kernel
-// leaves it zero again.
+// workgroup: slots and work units for all tokens; or the gate_up GEMM of a layer forward, which plans for itself).
+// DecodeState is zero when a call starts, and whichever kernel consumes it leaves it zero again.
 
 // With qx.x set, the workgroup of token t first writes the A8 of x's row t (H = 2048: wave w takes columns
 // 512 w .. 512 w + 511), so routing from given logits needs no launch of its own for it.
@@ -266,113 +248,20 @@ __global__ void __launch_bounds__(256) score_kernel(const float* __restrict__ pa
     if (pool_on) atomicMax(&blockmax[size_t(t / block) * E + e], okey(sg + bias[e]));
 }
 
-struct DecodeState {
-    uint32_t* blockmax;   // [E] ordered keys of max_t (sigmoid + bias)
-    uint32_t* tmask;      // [E] bit t: token t picked the expert
-};
 
-// Slots and work units of the decode step (engine/ops.cu:333-370), one workgroup of 256 threads.
-
-// Slots: expert-major, token-ascending; shared slots T K + t. Units: items of 16 slots split into row blocks by
-// code width, longest first (2 / 3 / 4 / 8-bit experts, then the shared expert).
+// Slots and work units of the decode step (engine/ops.cu:333-370), one workgroup of 256 threads (thread e writes
+// expert e's units); the masks and pool maxima are left zero for the next call.
 __global__ void __launch_bounds__(256) dispatch_kernel(int T, int E, int K, const int* __restrict__ topk,
                                                        const float* __restrict__ topw, DecodeState ds, DispatchOut d) {
-    __shared__ uint32_t m_s[MAXE];
-    __shared__ int start_s[MAXE];
-    __shared__ int wt_i[4];
-    __shared__ uint64_t wt_g[4], wt_d[4];
-    __shared__ uint64_t tot_g, tot_d;
+    __shared__ DecodePlan P;
+    decode_plan_scan(E, ds.tmask, d.bits, P);
     const int e = threadIdx.x;
-    const uint32_t m = e < E ? ds.tmask[e] : 0u;
-    // the (token, k) pairs of the placement below (T K <= 256: at most one per thread), read up front so that
-    // their latency overlaps the scans
-    const int ex0 = e < T * K ? topk[e] : 0;
-    const float w0 = e < T * K ? topw[e] : 0.0f;
     if (e < E) {
-        m_s[e] = m;
         ds.tmask[e] = 0u;
         ds.blockmax[e] = 0u;
+        decode_plan_write_expert(P, e, 0, 1, d);
     }
-    const int c = __popc(m);
-    const int bw = e < E ? d.bits[e] : 2;
-    const int nit = (c + 15) >> 4;
-    const int cls = decode_class(bw);
-    const uint64_t vg = uint64_t(nit * gemm_row_blocks(false, bw)) << (16 * cls);
-    const uint64_t vd = uint64_t(nit * gemm_row_blocks(true, bw)) << (16 * cls);
-    int incl = c;
-    uint64_t ig = vg, id = vd;
-    {   // three inclusive scans over the 256 threads in one pass: wave shuffles, then the wave totals
-        const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-        incl = wave_incl_scan(incl);
-        ig = wave_incl_scan(ig);
-        id = wave_incl_scan(id);
-        if (lane == 63) {
-            wt_i[w] = incl;
-            wt_g[w] = ig;
-            wt_d[w] = id;
-        }
-        __syncthreads();
-        for (int i = 0; i < w; ++i) {
-            incl += wt_i[i];
-            ig += wt_g[i];
-            id += wt_d[i];
-        }
-    }
-    if (e == 255) {
-        tot_g = ig;
-        tot_d = id;
-    }
-    const int st = incl - c;
-    if (e < E) start_s[e] = st;
-    __syncthreads();
-    const int sbits = d.has_shared ? d.bits[E] : 8;
-    const int ns = d.has_shared ? (T + 15) >> 4 : 0;
-    const int srg = gemm_row_blocks(false, sbits), srd = gemm_row_blocks(true, sbits);
-    // class bases: classes 0 .. 3, then the shared expert's units
-    int bg = 0, bd = 0, og = 0, od = 0;
-    for (int k = 0; k < 4; ++k) {
-        if (k == cls) {
-            og = bg + int(((ig - vg) >> (16 * k)) & 0xFFFFu);
-            od = bd + int(((id - vd) >> (16 * k)) & 0xFFFFu);
-        }
-        bg += int((tot_g >> (16 * k)) & 0xFFFFu);
-        bd += int((tot_d >> (16 * k)) & 0xFFFFu);
-    }
-    if (e < E) {
-        d.count[e] = c;
-        d.start[e] = st;
-        const int rg = gemm_row_blocks(false, bw), rd = gemm_row_blocks(true, bw);
-        for (int j = 0; j < nit; ++j) {
-            const int s0 = st + 16 * j, n = min(16, c - 16 * j);
-            for (int r = 0; r < rg; ++r) d.units_gu[og + j * rg + r] = Item{e, s0, n, r};
-            for (int r = 0; r < rd; ++r) d.units_dn[od + j * rd + r] = Item{e, s0, n, r};
-        }
-    }
-    for (int u = e; u < ns * srg; u += 256) units_shared(d.units_gu + bg, u, srg, E, T, K);
-    for (int u = e; u < ns * srd; u += 256) units_shared(d.units_dn + bd, u, srd, E, T, K);
-    if (e == 0) {
-        d.n_units[0] = bg + ns * srg;
-        d.n_units[1] = bd + ns * srd;
-        d.n_units[2] = 0;
-        d.n_units[3] = 0;
-    }
-    // place every (token, k) pair
-    for (int p = e; p < T * K; p += 256) {
-        const int t = p / K;
-        const int ex = p == e ? ex0 : topk[p];
-        const float w = p == e ? w0 : topw[p];
-        const int sl = start_s[ex] + __popc(m_s[ex] & ((1u << t) - 1u));
-        d.slot_token[sl] = t;
-        d.slot_weight[sl] = w;
-        d.tok_slots[p + t] = sl;                      // [t][k] of the [T][K + 1] table
-    }
-    if (e < T) {
-        if (d.has_shared) {
-            d.slot_token[T * K + e] = e;
-            d.slot_weight[T * K + e] = 1.0f;
-        }
-        d.tok_slots[size_t(e) * (K + 1) + K] = d.has_shared ? T * K + e : -1;
-    }
+    decode_plan_write_rest(P, e, 256, T, E, K, topk, topw, d);
 }
 
 
@@ -794,7 +683,7 @@ hipError_t launch_decode_route(const float* part, int nchunks, const float* bias
                                float rscale, float* sig, int32_t* topk, float* topw, uint32_t* blockmax,
                                uint32_t* tmask, int has_shared, const int8_t* bits, int32_t* count, int32_t* start,
                                Item* units_gu, Item* units_dn, int* n_units, int32_t* slot_token, float* slot_weight,
-                               int32_t* tok_slots, const QuantX& qx, hipStream_t st) {
+                               int32_t* tok_slots, const QuantX& qx, int dispatch, hipStream_t st) {
     if (T > 32 || E > MAXE) return hipErrorInvalidValue;
     const DecodeState ds{blockmax, tmask};
     if (C < E) {
@@ -811,7 +700,19 @@ hipError_t launch_decode_route(const float* part, int nchunks, const float* bias
     }
     const DispatchOut d{has_shared, 16, bits, count, start, units_gu, units_dn, n_units, slot_token, slot_weight,
                         tok_slots};
-    dispatch_kernel<<<1, 256, 0, st>>>(T, E, K, topk, topw, ds, d);
+    if (dispatch) dispatch_kernel<<<1, 256, 0, st>>>(T, E, K, topk, topw, ds, d);
+    return hipGetLastError();
+}
+
+__global__ void __launch_bounds__(256) zero_u32_kernel(uint32_t* __restrict__ a, uint32_t* __restrict__ b, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        a[i] = 0u;
+        b[i] = 0u;
+    }
+}
+
+hipError_t launch_zero_decode_state(uint32_t* blockmax, uint32_t* tmask, int E, hipStream_t st) {
+    zero_u32_kernel<<<1, 256, 0, st>>>(blockmax, tmask, E);
     return hipGetLastError();
 }
 

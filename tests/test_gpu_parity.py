@@ -219,6 +219,58 @@ def test_other_expert_counts(gpu, E, K, T, pool):
     G.close()
 
 
+def _decode_state(G, T, K, E, shared):
+    """Every buffer a decode step writes, as numpy arrays (the gate_up unit list up to its count)."""
+    S = T * K + (T if shared else 0)
+    n = G.read("n_items", (4,), np.int32)
+    st = {"n_items": n, "items": G.read("items", (int(n[0]), 4), np.int32)}
+    for name, shape, dt in (("topk", (T, K), np.int32), ("topw", (T, K), np.float32), ("count", (E,), np.int32),
+                            ("start", (E,), np.int32), ("slot_token", (S,), np.int32),
+                            ("slot_weight", (S,), np.float32), ("tok_slots", (T, K + 1), np.int32),
+                            ("Z", (S, 512), np.uint16), ("zq", (S, 512), np.int8), ("zs", (S, 4), np.float32),
+                            ("zsum", (S, 4), np.int32), ("Y", (S, 2048), np.float32)):
+        st[name] = G.read(name, shape, dt)
+    return st
+
+
+@pytest.mark.parametrize("E,K,T,pool,mix,shared", [
+    (256, 8, 32, 256, "mixed", True),   # config 1
+    (256, 8, 32, 48, 4, False),         # config 0 (pool)
+    (256, 8, 1, 256, "mixed", True),
+    (256, 8, 17, 48, "mixed", True),    # two shared items, pool
+    (64, 4, 32, 16, "mixed", True),
+    (128, 6, 5, 256, 8, False),
+])
+def test_decode_forward_plans_like_dispatch(gpu, E, K, T, pool, mix, shared):
+    """A decode layer forward plans the slots inside its gate_up GEMM (no dispatch kernel): every buffer, the gate_up
+    unit list and the output equal those of route + experts (the dispatch kernel's plan), bit for bit; a re-launch of
+    the gate_up stage from the written list reproduces Z; and a second forward (the down GEMM cleared the routing
+    masks) matches a fresh route + experts again."""
+    import torch
+    say(f"[decode plan] E={E} K={K} T={T} pool={pool} mix={mix} shared={shared}")
+    L = synth.make_layer(700 + E + K + T, E=E, mix=mix, shared=shared)
+    x = [synth.make_x(720 + T + i, T) for i in range(2)]
+    G = make_gpu_layer(L, pool, max_tokens=64, K=K)
+    R = make_gpu_layer(L, pool, max_tokens=64, K=K)
+    for i in range(2):
+        out = run_layer(G, x[i], gpu)
+        a = _decode_state(G, T, K, E, shared)
+        R.route(T, x=to_dev(x[i], gpu))
+        xq = G.read("xq", (T, 2048), np.int8)
+        xs = G.read("xs", (T, 16), np.float32)
+        xsum = G.read("xsum", (T, 16), np.int32)
+        ref = R.experts(to_dev(xq, gpu), to_dev(xs, gpu), to_dev(xsum, gpu))
+        torch.cuda.synchronize()
+        r = _decode_state(R, T, K, E, shared)
+        for name in r:
+            assert np.array_equal(a[name].view(np.uint8), r[name].view(np.uint8)), f"forward {i}: {name} differs"
+        assert np.array_equal(out.view(np.uint32), ref.cpu().numpy().view(np.uint32)), f"forward {i}: out differs"
+        G.time_stage("gate_up", 2)
+        assert np.array_equal(G.read("Z", a["Z"].shape, np.uint16), a["Z"]), "gate_up re-launch differs"
+    G.close()
+    R.close()
+
+
 @pytest.mark.parametrize("kind,T,pool", [
     ("zipf", 128, 256), ("skewed", 128, 256),
     ("zipf", 32, 256),    # one routing block: the decode kernels
