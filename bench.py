@@ -3,15 +3,16 @@
 
 Headline workload (value): config 1 -- one MoE layer, 32 tokens (one denoising block), hidden 2048, 256
 routed experts at the shipped 2/3/4-bit mix (61/34/6 %), uniform-random top-8 of sigmoid(x Wr), plus the W8A8
-shared expert; a step is one full layer pass (A8 of x -> router -> routing + dispatch -> gate_up -> FWHT-512 + A8
--> down -> combine) with x already resident in HBM. Also measured (fields "configs"): config 0 (32 tokens, all
+shared expert; a step is one full layer pass (A8 of x -> router -> routing -> gate_up (which also builds the slot
+plan) -> FWHT-512 + A8 -> down -> combine) with x already resident in HBM. Also measured (fields "configs"): config 0 (32 tokens, all
 4-bit, block pool 48, no shared expert), config 2 (512 tokens), config 3 (2048 tokens through a stack of 20
 independently seeded layers with Zipf(1.1) expert load), config 4 (4096 tokens at 2/4/8 bits, uniform and skewed
 routing) and the dense projection at 32 and 2048 tokens.
 
-Roofline: the dominant kernel is the gate_up expert GEMM (two thirds of the weight bytes); its algorithmic bytes
-per launch are the packed gate_up bytes of every expert the step touches (each streamed exactly once) plus the
-shared expert's, and its duration is measured with HIP events on the launch stream (llmoe_layer_stage_ms).
+Roofline: the dominant kernel is the gate_up expert GEMM (two thirds of the weight bytes; at decode the kernel that
+also plans the slots from the routing masks); its algorithmic bytes per launch are the packed gate_up bytes of every
+expert the step touches (each streamed exactly once) plus the shared expert's, and its duration is measured with
+HIP events on the launch stream (re-launches of the step's own gate_up kernel, llmoe_layers_time_stage).
 
 CPU baseline: the CPU oracle (oracle/, the C restatement of the reference's path, OpenMP over experts) timed on
 the host cores on the same config-1 layer and input, repeated for a bounded ~10 s.
@@ -502,7 +503,7 @@ def main():
     achieved = c1["gate_up_bytes"] / gu_s / 1e9
     roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": achieved / PEAK_HBM_GBS, "traffic": measured_traffic(),
-                "kernel": "expert_gemm<gate_up> (config 1)", "bytes_per_launch": c1["gate_up_bytes"],
+                "kernel": "expert_gemm_plan (config 1: the decode gate_up GEMM, planning its units)", "bytes_per_launch": c1["gate_up_bytes"],
                 "avg_launch_ms": p["gate_up"]}
     cpu = None
     if not args.no_cpu:

@@ -122,6 +122,9 @@ struct llmoe_layer {
     bool ran[LLMOE_N_STAGES] = {};
     // the latest llmoe_experts launch (for llmoe_layer_time_stage)
     GemmArgs last_gu{}, last_dn{}, last_tgu{}, last_tdn{};
+    bool last_plan = false;                         // the latest gate_up planned for itself (launch_expert_gemm_plan)
+    DecodePlanArgs last_pa{};                       // its arguments, planning from the copy of the masks
+    uint32_t* tcopy = nullptr;                      // [E] the masks of the latest self-planned gate_up
     float* last_out = nullptr;
     NormOut last_norm{};
     Inter last_w{};
@@ -355,6 +358,7 @@ int llmoe_layer_create(const llmoe_layer_desc* desc, const void* blob, size_t bl
     // kernel that consumes them (place_kernel, dispatch_kernel)
     ALLOC(L->blockmax, nbm * E);
     ALLOC(L->tmask, E);
+    ALLOC(L->tcopy, E);
 
     if (hipMemset(L->blockmax, 0, nbm * E * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(L->mask, 0, nbm * E * sizeof(uint32_t)) != hipSuccess ||
@@ -467,6 +471,10 @@ int llmoe_dispatch(llmoe_layer* L, const int32_t* topk, const float* topw, int T
     const auto& d = L->d;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     L->routed_T = -1;
+    if (L->plan_pending) {   // a forward's routing masks that no expert call consumed
+        L->plan_pending = false;
+        HIPCHECK(launch_zero_decode_state(L->blockmax, L->tmask, d.n_experts, st));
+    }
     if (int rc = prepare_items(L, T)) return rc;
     HIPCHECK(hipMemcpyAsync(L->topk, topk, size_t(T) * d.top_k * sizeof(int32_t), hipMemcpyDeviceToDevice, st));
     HIPCHECK(hipMemcpyAsync(L->topw, topw, size_t(T) * d.top_k * sizeof(float), hipMemcpyDeviceToDevice, st));
@@ -507,11 +515,14 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     // that the dispatch kernel would have (re-launches for stage timing then read those lists)
     const bool plan = L->plan_pending && !L->tiled;
     L->plan_pending = false;
+    L->last_plan = plan;
     L->mark(LLMOE_STAGE_GATE_UP, false, st);
     if (plan) {
-        const DecodePlanArgs pa{T, d.n_experts, K, L->tmask, L->topk, L->topw,
+        const DecodePlanArgs pa{T, d.n_experts, K, L->tmask, L->tcopy, L->topk, L->topw,
                                 DispatchOut{d.has_shared, 16, L->bits_d, L->count, L->start, L->units_gu, L->units_dn,
                                             L->n_units, L->slot_token, L->slot_weight, L->tok_slots}};
+        L->last_pa = pa;
+        L->last_pa.tmask = L->tcopy;   // a re-launch plans from the copy
         HIPCHECK(launch_expert_gemm_plan(g, pa, st));
     } else {
         HIPCHECK(launch_gemm(GEMM_GATE_UP, g, tg, L->tiled, st));
@@ -653,7 +664,9 @@ namespace {
 hipError_t relaunch_stage(llmoe_layer* L, int stage, hipStream_t st) {
     const auto& d = L->d;
     switch (stage) {
-        case LLMOE_STAGE_GATE_UP: return launch_gemm(GEMM_GATE_UP, L->last_gu, L->last_tgu, L->last_tiled, st);
+        case LLMOE_STAGE_GATE_UP:   // the kernel the call ran (a decode forward's plans again, from the copied masks)
+            return L->last_plan ? launch_expert_gemm_plan(L->last_gu, L->last_pa, st)
+                                : launch_gemm(GEMM_GATE_UP, L->last_gu, L->last_tgu, L->last_tiled, st);
         case LLMOE_STAGE_DOWN: return launch_gemm(GEMM_DOWN, L->last_dn, L->last_tdn, L->last_tiled, st);
         case LLMOE_STAGE_FWHT:
             // one routing block: FWHT-512 + A8 runs inside the streamed down GEMM (its time is in that stage)

@@ -193,6 +193,7 @@ __device__ __forceinline__ void decode_plan_write_rest(const DecodePlan& P, int 
 struct DecodePlanArgs {   // the self-planning gate_up GEMM's routing inputs and plan outputs
     int T, E, K;
     const uint32_t* tmask;
+    uint32_t* tcopy;     // [E] the masks planned from, kept for a re-launch (the down GEMM zeroes tmask)
     const int32_t* topk;
     const float* topw;
     DispatchOut d;

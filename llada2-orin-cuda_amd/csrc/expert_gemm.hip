@@ -457,8 +457,8 @@ __global__ void __launch_bounds__(WAVES * 64, NT == 1 ? 3 : 1) expert_gemm(GemmA
 // The decode gate_up GEMM of a layer forward, planning for itself: every workgroup builds the slot plan in LDS from
 // the routing masks (decode_plan.h) and takes the units blockIdx.x, blockIdx.x + gridDim.x, ... of the gate_up list
 // that the dispatch kernel would have written; workgroups G - 1 - r, r = 0 .. E, write the plan's lists first (expert
-// r's units, or the shared units and the placement), for the down GEMM, the combine and the buffers' readers. The routing masks
-// stay as they are (the down GEMM zeroes them).
+// r's units, or the shared units and the placement), for the down GEMM, the combine and the buffers' readers, and a
+// copy of the masks (tcopy) from which a re-launch plans the same units after the down GEMM has zeroed them.
 __global__ void __launch_bounds__(WAVES * 64, 3) expert_gemm_plan(GemmArgs a, DecodePlanArgs p) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ DecodePlan P;
@@ -467,8 +467,12 @@ __global__ void __launch_bounds__(WAVES * 64, 3) expert_gemm_plan(GemmArgs a, De
     // the writer roles go to the last workgroups, whose units are in the first round only (config 1: 56.8 -> 56.2 us
     // against the first workgroups)
     for (int r = int(gridDim.x - 1 - blockIdx.x); r <= p.E; r += gridDim.x) {
-        if (r < p.E) decode_plan_write_expert(P, r, threadIdx.x, blockDim.x, p.d);
-        else decode_plan_write_rest(P, threadIdx.x, blockDim.x, p.T, p.E, p.K, p.topk, p.topw, p.d);
+        if (r < p.E) {
+            decode_plan_write_expert(P, r, threadIdx.x, blockDim.x, p.d);
+        } else {
+            decode_plan_write_rest(P, threadIdx.x, blockDim.x, p.T, p.E, p.K, p.topk, p.topw, p.d);
+            if (threadIdx.x < p.E) p.tcopy[threadIdx.x] = P.m[threadIdx.x];
+        }
     }
     const int n = decode_plan_units(P, false, p.T, p.d.has_shared, sbits);
     const RowSrc rs{&P, p.T, p.K, p.E};

@@ -361,7 +361,7 @@ def test_full_size_batch_invariance(gpu, T, mix, shared, pool, kind):
     assert np.array_equal(out[rows].view(np.uint32), r["out"].view(np.uint32)), "output rows not bit-exact"
 
 
-@pytest.mark.parametrize("T,pool", [(32, 256), (200, 48)])
+@pytest.mark.parametrize("T,pool", [(32, 256), (32, 48), (200, 48)])
 def test_experts_norm_bit_exact(gpu, T, pool):
     """llmoe_experts_norm: combine + FWHT-2048 un-rotation + residual + next-layer RMSNorm / rotation / A8."""
     import torch
@@ -468,7 +468,7 @@ def test_external_dispatch(gpu):
     G.close()
 
 
-@pytest.mark.parametrize("T,pool", [(32, 256), (200, 48)])
+@pytest.mark.parametrize("T,pool", [(32, 256), (32, 48), (200, 48)])
 def test_hip_graph_replays(gpu, T, pool):
     """The layer forward and a dense projection captured in one HIP graph: every replay, with eager calls on other
     inputs and host synchronisations in between, reproduces the eager results bit for bit (the calls allocate,
