@@ -119,7 +119,9 @@ int llmoe_experts_norm(llmoe_layer* layer, const int8_t* xq, const float* xs, co
 int llmoe_experts_scratch(llmoe_layer* layer, const int8_t* xq, const float* xs, const int32_t* xsum, int T,
                           float* out, llmoe_stream stream);
 
-/* Whole layer: A8(x) -> route (x Wr, or the given logits) -> experts -> out. x fp32 [T, H]. */
+/* Whole layer: A8(x) -> route (x Wr, or the given logits) -> experts -> out. x fp32 [T, H]. At decode (T <= block)
+ * the slot plan is built inside the gate_up GEMM rather than by a dispatch kernel; the results and the buffers
+ * (llmoe_layer_buffers) are the same as route + experts. */
 int llmoe_layer_forward(llmoe_layer* layer, const float* x, const float* logits, int T, float* out,
                         llmoe_stream stream);
 
