@@ -566,30 +566,33 @@ __global__ void __launch_bounds__(PLAN_NT) plan_kernel(const uint32_t* __restric
     // (pre[j] <= lo_q < pre[j + 1]) is found by binary search, and the task inside it is the first row block
     // whose cost span (after the chunk's staging cost) starts at or after lo_q (one past the chunk's last: the
     // next chunk's first)
-    for (int m = 0; m < 2; ++m) {
+    // (both GEMMs' partitions at once: thread i takes workgroup i of gate_up, or i - g_gu of down)
+    if (tid == 0) {
+        tstart[g_gu] = n;
+        tstart[g_gu + 1 + g_dn] = n;
+    }
+    for (int idx = tid; idx < g_gu + g_dn; idx += blockDim.x) {
+        const int m = idx >= g_gu, q = m ? idx - g_gu : idx;
         const int G = m ? g_dn : g_gu;
         const int* P = m ? pre_dn : pre_gu;
         const uint32_t* task = m ? task_dn : task_gu;
         int* ts = tstart + (m ? g_gu + 1 : 0);
         const long long C = P[n];
-        if (tid == 0) ts[G] = n;
-        for (int q = tid; q < G; q += blockDim.x) {
-            const long long lo = C == 0 ? 0 : floor_div((long long)q * C + G - 1, G);
-            if (lo >= C) {
-                ts[q] = n;
-                continue;
-            }
-            int a = 0, b = n;   // P[a] <= lo < P[b]
-            while (b - a > 1) {
-                const int mid = (a + b) >> 1;
-                if (P[mid] <= lo) a = mid;
-                else b = mid;
-            }
-            const int nrb = int(task[a] & 255u), span = int(task[a] >> 8);
-            const long long off = lo - P[a] - (m ? STAGE_COST_DN : STAGE_COST_GU);
-            const int r = off <= 0 ? 0 : int((off + span - 1) / span);
-            ts[q] = r >= nrb ? a + 1 : (a | (r << TASK_RB_SHIFT));
+        const long long lo = C == 0 ? 0 : floor_div((long long)q * C + G - 1, G);
+        if (lo >= C) {
+            ts[q] = n;
+            continue;
         }
+        int a = 0, b = n;   // P[a] <= lo < P[b]
+        while (b - a > 1) {
+            const int mid = (a + b) >> 1;
+            if (P[mid] <= lo) a = mid;
+            else b = mid;
+        }
+        const int nrb = int(task[a] & 255u), span = int(task[a] >> 8);
+        const long long off = lo - P[a] - (m ? STAGE_COST_DN : STAGE_COST_GU);
+        const int r = off <= 0 ? 0 : int((off + span - 1) / span);
+        ts[q] = r >= nrb ? a + 1 : (a | (r << TASK_RB_SHIFT));
     }
 }
 
