@@ -271,6 +271,40 @@ def test_decode_forward_plans_like_dispatch(gpu, E, K, T, pool, mix, shared):
     R.close()
 
 
+def test_decode_forward_plans_like_dispatch_random(gpu):
+    """The self-planning decode forward against route + experts on 24 seeded draws of the shape (E, top-K, T from 1
+    to 32, pool or not, shared expert or not, code mix): every buffer, the gate_up unit list and the output bit for
+    bit, on one layer object per shape and three consecutive forwards (the routing masks are cleared in between)."""
+    import torch
+    rng = np.random.default_rng(2024)
+    for case in range(24):
+        E = int(rng.choice([64, 128, 256]))
+        K = int(rng.integers(2, 9))
+        T = int(rng.integers(1, 33))
+        pool = int(rng.choice([E, 48, 16])) if E > 48 else E
+        shared = bool(rng.integers(0, 2))
+        mix = ["mixed", 2, 3, 4, 8][int(rng.integers(0, 5))]
+        say(f"[decode plan random {case}] E={E} K={K} T={T} pool={pool} shared={shared} mix={mix}")
+        # one matrix per code width, the other experts aliasing it: every expert keeps its width (the plan's classes)
+        L = synth.make_layer(5000 + case, E=E, mix=mix, shared=shared, experts=[0])
+        G = make_gpu_layer(L, pool, max_tokens=32, K=K)
+        R = make_gpu_layer(L, pool, max_tokens=32, K=K)
+        for i in range(3):
+            x = synth.make_x(6000 + 10 * case + i, T)
+            out = run_layer(G, x, gpu)
+            a = _decode_state(G, T, K, E, shared)
+            R.route(T, x=to_dev(x, gpu))
+            ref = R.experts(to_dev(G.read("xq", (T, 2048), np.int8), gpu), to_dev(G.read("xs", (T, 16), np.float32), gpu),
+                            to_dev(G.read("xsum", (T, 16), np.int32), gpu))
+            torch.cuda.synchronize()
+            r = _decode_state(R, T, K, E, shared)
+            for name in r:
+                assert np.array_equal(a[name].view(np.uint8), r[name].view(np.uint8)), f"case {case} forward {i}: {name}"
+            assert np.array_equal(out.view(np.uint32), ref.cpu().numpy().view(np.uint32)), f"case {case} forward {i}: out"
+        G.close()
+        R.close()
+
+
 @pytest.mark.parametrize("kind,T,pool", [
     ("zipf", 128, 256), ("skewed", 128, 256),
     ("zipf", 32, 256),    # one routing block: the decode kernels
