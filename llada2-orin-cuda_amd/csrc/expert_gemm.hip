@@ -159,8 +159,20 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, con
     const int sbase = row_block * WAVES * SPW;
     auto step_ptr = [&](int u) { return mat_e + (size_t(sbase + (u / NSB) * WAVES + wave) * NSB + (u % NSB)) * SBB; };
 
-    // weight prefetch first: its latency overlaps the meta and B staging below
+    // weight prefetch first: its latency overlaps the meta and B staging below (the down GEMM's Z rows, whose
+    // addresses need no load, are requested before it, so their transform overlaps the ring fill)
     Step<BITS> ring[D];
+    constexpr bool ZIN = MODE == GEMM_DOWN;
+    constexpr int PERW = NTOK / WAVES;
+    uint4 zraw[ZIN ? PERW : 1];
+    if (ZIN && a.zin != nullptr) {
+#pragma unroll
+        for (int i = 0; i < PERW; ++i) {
+            const int n = wave + i * WAVES;
+            zraw[i] = n < it.ntok ? *reinterpret_cast<const uint4*>(a.zin + size_t(it.slot0 + n) * K + 8 * lane)
+                                  : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
 #pragma unroll
     for (int u = 0; u < D; ++u)
         if (u < NSTEP) load_step<BITS>(step_ptr(u), lane, ring[u]);
@@ -178,15 +190,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, con
         // B rows = A8(FWHT-512(Z)) of the item's slots, slot n on wave n % WAVES (the operations of
         // fwht_a8_kernel); the units of row block 0 also store them for the buffers' readers. Rows n >= ntok are
         // zero. The wave's Z rows are all loaded before the first transform, so their latencies overlap.
-        constexpr int PERW = NTOK / WAVES;
         static_assert(PERW * WAVES == NTOK, "slots per wave");
-        uint4 zraw[PERW];
-#pragma unroll
-        for (int i = 0; i < PERW; ++i) {
-            const int n = wave + i * WAVES;
-            zraw[i] = n < ntok ? *reinterpret_cast<const uint4*>(a.zin + size_t(it.slot0 + n) * K + 8 * lane)
-                               : make_uint4(0u, 0u, 0u, 0u);
-        }
 #pragma unroll
         for (int i = 0; i < PERW; ++i) {
             const int n = wave + i * WAVES;
