@@ -70,6 +70,32 @@ __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ Y
     int sl[MAX_KK];   // (scalar loads: the row's slots are the same for the whole workgroup)
 #pragma unroll
     for (int k = 0; k < MAX_KK; ++k) sl[k] = k < kk ? *const_ptr(tok_slots + t * K1 + k) : 0;
+    if constexpr (HALF) {
+        // fp16 rows: 8 columns (16 bytes of each row) per thread and pass, the same ordered sums
+        for (int hb = h0 + threadIdx.x * 8; hb < h1; hb += blockDim.x * 8) {
+            uint4 raw[MAX_KK];
+#pragma unroll
+            for (int k = 0; k < MAX_KK; ++k)
+                if (k < kk)
+                    raw[k] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(Y) + size_t(sl[k]) * H + hb);
+            float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int k = 0; k < MAX_KK; ++k) {
+                if (k < kk) {
+                    const uint32_t w[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        acc[2 * j] = acc[2 * j] + f16_bits_to_f32(w[j] & 0xFFFFu);
+                        acc[2 * j + 1] = acc[2 * j + 1] + f16_bits_to_f32(w[j] >> 16);
+                    }
+                }
+            }
+            float4* o = reinterpret_cast<float4*>(out + size_t(t) * H + hb);
+            o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        }
+        return;
+    }
     // R float4 columns per thread per pass: every load of the pass is in flight before the ordered sums
     constexpr int R = 2;
     for (int hb = h0 + threadIdx.x * 4; hb < h1; hb += blockDim.x * 4 * R) {
