@@ -139,8 +139,10 @@ int llmoe_dense_forward(llmoe_dense* D, const int8_t* xq, const float* xs, const
     if (T < 1 || T > D->max_tokens) return dfail(LLMOE_EINVAL, "T = %d outside [1, max_tokens = %d]", T, D->max_tokens);
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const bool tiled = T > 32;
-    dense_plan_kernel<<<1, 256, 0, st>>>(T, D->R, D->bits, tiled ? 1 : 0, D->G, D->units, D->n_units, D->tstart);
-    DHIP(hipGetLastError());
+    if (tiled) {   // (streamed: the GEMM computes its units from T and R itself)
+        dense_plan_kernel<<<1, 256, 0, st>>>(T, D->R, D->bits, 1, D->G, D->units, D->n_units, D->tstart);
+        DHIP(hipGetLastError());
+    }
     GemmArgs g{};
     g.base = D->arena;
     g.off = D->off;
@@ -156,6 +158,10 @@ int llmoe_dense_forward(llmoe_dense* D, const int8_t* xq, const float* xs, const
     g.Y = y;
     g.tstart = D->tstart;
     g.accumulate = accumulate ? 1 : 0;
+    if (!tiled) {
+        g.dense_T = T;
+        g.dense_nrb = D->R / (16 * GEMM_WAVES * gemm_spw(false, D->bits));
+    }
     DHIP(tiled ? launch_tiled_gemm(GEMM_DENSE, g, st) : launch_expert_gemm(GEMM_DENSE, 1, g, 0, st));
     return LLMOE_OK;
 }

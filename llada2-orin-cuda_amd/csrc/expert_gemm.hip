@@ -442,10 +442,19 @@ __global__ void __launch_bounds__(WAVES * 64, NT == 1 ? 3 : 1) expert_gemm(GemmA
     // the unit and the expert's code width and matrix offset are read through the scalar cache (constant address
     // space: the lists are written by earlier kernels only), the width and offset together, so the weight stream
     // starts after two short dependent loads
-    const int n = *a.n_items;
+    // a dense projection's units follow from T and R: items of 16 tokens, each split into row blocks
+    const bool dense_t = MODE == GEMM_DENSE && a.dense_T > 0;
+    const int nrb_d = dense_t ? a.dense_nrb : 1;
+    const int n = dense_t ? ((a.dense_T + 15) >> 4) * nrb_d : *a.n_items;
     for (int u = blockIdx.x; u < n; u += gridDim.x) {
-        const auto* ip = const_ptr(reinterpret_cast<const int*>(a.items + u));
-        const Item it{ip[0], ip[1], ip[2], ip[3]};
+        Item it;
+        if (dense_t) {
+            const int j = u / nrb_d;
+            it = Item{0, 16 * j, min(16, a.dense_T - 16 * j), u - j * nrb_d};
+        } else {
+            const auto* ip = const_ptr(reinterpret_cast<const int*>(a.items + u));
+            it = Item{ip[0], ip[1], ip[2], ip[3]};
+        }
         const uint64_t off = *const_ptr(a.off + it.expert);
         const uint32_t bw4 = *const_ptr(reinterpret_cast<const uint32_t*>(a.bits) + (it.expert >> 2));
         asm volatile("" ::"s"(off), "s"(bw4));   // both loads in flight together, before the branch on the width

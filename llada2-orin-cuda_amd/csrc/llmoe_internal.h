@@ -351,6 +351,8 @@ struct GemmArgs {
     int32_t* P;                 // group-products out [n, R, K/128] (test entry)
     const int* tstart;          // tiled: [G + 1] first task of each workgroup (the work partition above)
     int accumulate;             // GEMM_DENSE: Y += acc instead of Y = acc
+    int dense_T;                // streamed GEMM_DENSE: the tokens, units computed in the kernel (items unused); 0: items
+    int dense_nrb;              // ... and the row blocks of the matrix (R / (16 GEMM_WAVES spw))
     int fast;                   // gate_up: SiLU by the hardware exp / reciprocal and fp16 conversion
     // streamed down GEMM: with zin set, the B rows are staged as A8(FWHT-512(zin[slot])) instead of read from xq / xs /
     // xsum, and the units of row block 0 also write those rows to xq_out / xs_out / xsum_out
