@@ -358,6 +358,28 @@ def dense_config(llmoe, synth, torch, R, bits, T, steps, warmup, nmat=40):
     xq, xs, xsum = llmoe.quantize_a8(torch.from_numpy(synth.make_x(9, T)).to(dev))
     y = torch.empty((T, R), dtype=torch.float32, device=dev)
     dt = time_steps(lambda i: Ds[i % nmat].forward(xq, xs, xsum, out=y), steps, warmup)
+    # GPU time per projection: one projection per matrix captured back to back in a HIP graph, replayed (a Python
+    # call per projection costs more host time than a 32-token projection takes on the GPU)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for D in Ds:
+            D.forward(xq, xs, xsum, out=y)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for D in Ds:
+            D.forward(xq, xs, xsum, out=y)
+    reps = max(3, steps // nmat)
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    t_gpu = (time.perf_counter() - t0) / (reps * nmat)
+    del g
     for D in Ds:
         D.close()
     t = dt / steps
@@ -365,7 +387,9 @@ def dense_config(llmoe, synth, torch, R, bits, T, steps, warmup, nmat=40):
     return {"workload": f"dense W{bits}A8 projection [{R} x {H}] (qkv shape), {T} tokens", "tokens": T,
             "ms_per_step": t * 1e3, "tokens_per_s": T / t, "weight_bytes": wb, "weight_stream_GBps": wb / t / 1e9,
             "weight_stream_frac_peak": wb / t / 1e9 / PEAK_HBM_GBS, "int8_TOPS": 2 * T * R * H / t / 1e12,
-            "int8_mfma_frac_peak": 2 * T * R * H / t / 1e12 / PEAK_INT8_TOPS}
+            "int8_mfma_frac_peak": 2 * T * R * H / t / 1e12 / PEAK_INT8_TOPS,
+            "graph_replay": {"us_per_projection": t_gpu * 1e6, "weight_stream_GBps": wb / t_gpu / 1e9,
+                             "weight_stream_frac_peak": wb / t_gpu / 1e9 / PEAK_HBM_GBS}}
 
 
 def cpu_threads():

@@ -45,21 +45,10 @@ int dfail(int code, const char* fmt, ...) {
         if (e_ != hipSuccess) return dfail(LLMOE_EHIP, "%s: %s", #expr, hipGetErrorString(e_));           \
     } while (0)
 
-// Work list of one call, one workgroup. Streamed: units {0, 16 j, n, r} for the items of 16 tokens and the
-// R / (16 GEMM_WAVES spw) row blocks. Tiled: chunks {0, j per, n, 0} and the partition of the nch nrb equal
+// Work list of a tiled call (T > 32), one workgroup: chunks {0, j per, n, 0} and the partition of the nch nrb equal
 // (chunk, row block) tasks: workgroup w starts at task ceil(w N / G) (chunk | rb << TASK_RB_SHIFT).
-__global__ void __launch_bounds__(256) dense_plan_kernel(int T, int R, int bits, int tiled, int G,
-                                                         Item* __restrict__ units, int* __restrict__ n_units,
-                                                         int* __restrict__ tstart) {
-    if (!tiled) {
-        const int nrb = R / (16 * GEMM_WAVES * gemm_spw(false, bits)), nit = (T + 15) / 16;
-        for (int u = threadIdx.x; u < nit * nrb; u += blockDim.x) {
-            const int j = u / nrb;
-            units[u] = Item{0, 16 * j, min(16, T - 16 * j), u % nrb};
-        }
-        if (threadIdx.x == 0) n_units[0] = nit * nrb;
-        return;
-    }
+__global__ void __launch_bounds__(256) dense_plan_kernel(int T, int R, int bits, int G, Item* __restrict__ units,
+                                                         int* __restrict__ n_units, int* __restrict__ tstart) {
     const int nch = tiled_chunks(T), per = tiled_per(T), nrb = R / (16 * tiled_waves(false) * tiled_spw(false, bits));
     for (int j = threadIdx.x; j < nch; j += blockDim.x) units[j] = Item{0, j * per, min(per, T - j * per), 0};
     const long long N = (long long)nch * nrb;
@@ -98,8 +87,7 @@ int llmoe_dense_create(int rows, int k, int bits, const uint8_t* blob, size_t bl
         return true;
     };
     uint8_t* staging = nullptr;
-    const size_t cap = std::max<size_t>(size_t((max_tokens + 15) / 16) * (rows / 64),
-                                        size_t(tiled_chunks(max_tokens)));
+    const size_t cap = size_t(tiled_chunks(max_tokens));
     bool ok = D->G > 0 && alloc(reinterpret_cast<void**>(&D->arena), bytes) &&
               alloc(reinterpret_cast<void**>(&D->off), sizeof(uint64_t)) &&
               alloc(reinterpret_cast<void**>(&D->bits_d), 4) &&   // a whole dword: read by scalar dword loads
@@ -139,8 +127,8 @@ int llmoe_dense_forward(llmoe_dense* D, const int8_t* xq, const float* xs, const
     if (T < 1 || T > D->max_tokens) return dfail(LLMOE_EINVAL, "T = %d outside [1, max_tokens = %d]", T, D->max_tokens);
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const bool tiled = T > 32;
-    if (tiled) {   // (streamed: the GEMM computes its units from T and R itself)
-        dense_plan_kernel<<<1, 256, 0, st>>>(T, D->R, D->bits, 1, D->G, D->units, D->n_units, D->tstart);
+    if (tiled) {   // (T <= 32: the split-K kernel needs no work list)
+        dense_plan_kernel<<<1, 256, 0, st>>>(T, D->R, D->bits, D->G, D->units, D->n_units, D->tstart);
         DHIP(hipGetLastError());
     }
     GemmArgs g{};
@@ -158,11 +146,8 @@ int llmoe_dense_forward(llmoe_dense* D, const int8_t* xq, const float* xs, const
     g.Y = y;
     g.tstart = D->tstart;
     g.accumulate = accumulate ? 1 : 0;
-    if (!tiled) {
-        g.dense_T = T;
-        g.dense_nrb = D->R / (16 * GEMM_WAVES * gemm_spw(false, D->bits));
-    }
-    DHIP(tiled ? launch_tiled_gemm(GEMM_DENSE, g, st) : launch_expert_gemm(GEMM_DENSE, 1, g, 0, st));
+    g.dense_T = T;
+    DHIP(tiled ? launch_tiled_gemm(GEMM_DENSE, g, st) : launch_dense_splitk(D->bits, g, st));
     return LLMOE_OK;
 }
 

@@ -393,15 +393,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, con
                 const int n = nt * 16 + col;
                 if (n < ntok) {
                     const int slot = it.slot0 + n;
-                    if constexpr (MODE == GEMM_DENSE) {
-                        float4* yp = reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q);
-                        float4 y = make_float4(acc[nt][0], acc[nt][1], acc[nt][2], acc[nt][3]);
-                        if (a.accumulate) {
-                            const float4 o = *yp;
-                            y = make_float4(o.x + y.x, o.y + y.y, o.z + y.z, o.w + y.w);
-                        }
-                        *yp = y;
-                    } else if constexpr (MODE == GEMM_GATE_UP) {
+                    if constexpr (MODE == GEMM_GATE_UP) {
                         // lane quad q holds rows gate 8 strip + 2q, up (same), gate + 1, up + 1
                         uint32_t z0, z1;
                         if (a.fast) {
@@ -442,19 +434,10 @@ __global__ void __launch_bounds__(WAVES * 64, NT == 1 ? 3 : 1) expert_gemm(GemmA
     // the unit and the expert's code width and matrix offset are read through the scalar cache (constant address
     // space: the lists are written by earlier kernels only), the width and offset together, so the weight stream
     // starts after two short dependent loads
-    // a dense projection's units follow from T and R: items of 16 tokens, each split into row blocks
-    const bool dense_t = MODE == GEMM_DENSE && a.dense_T > 0;
-    const int nrb_d = dense_t ? a.dense_nrb : 1;
-    const int n = dense_t ? ((a.dense_T + 15) >> 4) * nrb_d : *a.n_items;
+    const int n = *a.n_items;
     for (int u = blockIdx.x; u < n; u += gridDim.x) {
-        Item it;
-        if (dense_t) {
-            const int j = u / nrb_d;
-            it = Item{0, 16 * j, min(16, a.dense_T - 16 * j), u - j * nrb_d};
-        } else {
-            const auto* ip = const_ptr(reinterpret_cast<const int*>(a.items + u));
-            it = Item{ip[0], ip[1], ip[2], ip[3]};
-        }
+        const auto* ip = const_ptr(reinterpret_cast<const int*>(a.items + u));
+        const Item it{ip[0], ip[1], ip[2], ip[3]};
         const uint64_t off = *const_ptr(a.off + it.expert);
         const uint32_t bw4 = *const_ptr(reinterpret_cast<const uint32_t*>(a.bits) + (it.expert >> 2));
         asm volatile("" ::"s"(off), "s"(bw4));   // both loads in flight together, before the branch on the width
@@ -505,6 +488,90 @@ __global__ void __launch_bounds__(WAVES * 64, 3) expert_gemm_plan(GemmArgs a, De
     }
 }
 
+// Dense projection at T <= 32, split over K: workgroup (strip s, token tiles) computes 16 rows x 16 NTL tokens;
+// wave w loads only superblock w of the strip (groups 4w .. 4w + 3), with its B operands straight from x' (a few KiB,
+// resident in L2). Its exact group products P_g (the biased accumulator's float) and scale products sw sx go through
+// LDS; then wave v accumulates value v of every lane (rows 4q + v) over the 16 groups in ascending order: the fp32
+// sequence of the streamed GEMM, with four waves in flight per strip (NTL 16-token tiles per workgroup).
+template <int NTL>
+__host__ __device__ constexpr int dense_lds() { return NTL * 2 * 16 * 4 * 64 * 4 + WAVES * META_SB; }
+template <int BITS, int NTL>
+__global__ void __launch_bounds__(WAVES * 64) dense_splitk_kernel(GemmArgs a) {
+    static_assert(WAVES == 4, "one superblock per wave");
+    constexpr int G = 16;
+    constexpr size_t SBB = sb_bytes(BITS);
+    constexpr int ZOFF = BITS == 8 ? 128 : 0;
+    extern __shared__ __align__(16) uint8_t dl[];
+    float (*Ps)[G][4][64] = reinterpret_cast<float (*)[G][4][64]>(dl);                          // [NTL]
+    float (*Ss)[G][4][64] = reinterpret_cast<float (*)[G][4][64]>(dl + NTL * G * 4 * 64 * 4);   // [NTL]
+    uint8_t* meta = dl + 2 * NTL * G * 4 * 64 * 4;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, q = lane >> 4, col = lane & 15;
+    const int s = blockIdx.x, t0 = 16 * NTL * int(blockIdx.y);
+    Step<BITS> st;
+    load_step<BITS>(a.base + *const_ptr(a.off) + (size_t(s) * 4 + w) * SBB, lane, st);
+    v4i B0[NTL][4], B1[NTL][4];
+    float xsv[NTL][4];
+    int nxs[NTL][4];
+#pragma unroll
+    for (int tt = 0; tt < NTL; ++tt) {
+        // absent tokens read a present row; their outputs are not stored
+        const int tok = min(t0 + 16 * tt + col, a.dense_T - 1);
+#pragma unroll
+        for (int tau = 0; tau < 4; ++tau) {
+            const int g = 4 * w + tau;
+            const int8_t* br = a.xq + size_t(tok) * 2048 + g * GROUP + 16 * q;
+            B0[tt][tau] = *reinterpret_cast<const v4i*>(br);
+            B1[tt][tau] = *reinterpret_cast<const v4i*>(br + 64);
+            xsv[tt][tau] = a.xs[size_t(tok) * G + g];
+            nxs[tt][tau] = -a.xsum[size_t(tok) * G + g];
+        }
+    }
+    // the superblock's scales and zeros through the wave's LDS slot (as in gemm_body)
+    uint8_t* mp = meta + w * META_SB;
+    __builtin_amdgcn_wave_barrier();
+    if (lane < META_SB / 4) *reinterpret_cast<uint32_t*>(mp + 4 * lane) = st.m;
+    __builtin_amdgcn_wave_barrier();
+    const u4 ms0 = *reinterpret_cast<const u4*>(mp + 32 * q);
+    const u4 ms1 = *reinterpret_cast<const u4*>(mp + 32 * q + 16);
+    const u4 zw4 = *reinterpret_cast<const u4*>(mp + 128 + 16 * q);
+#pragma unroll
+    for (int tau = 0; tau < 4; ++tau) {
+        const int g = 4 * w + tau;
+        uint32_t Dw[8];
+        unpack_tile<BITS>(st, tau, Dw);
+        const v4i A0 = {int(Dw[0]), int(Dw[1]), int(Dw[2]), int(Dw[3])};
+        const v4i A1 = {int(Dw[4]), int(Dw[5]), int(Dw[6]), int(Dw[7])};
+        const uint32_t zw = zw4[tau];
+        const u4& sv = tau < 2 ? ms0 : ms1;
+        const uint32_t swp[2] = {wsel(sv, (tau & 1) * 2), wsel(sv, (tau & 1) * 2 + 1)};
+#pragma unroll
+        for (int tt = 0; tt < NTL; ++tt) {
+            v4i C;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) C[v] = __mul24(int((zw >> (8 * v)) & 0xFFu) - ZOFF, nxs[tt][tau]) + I2F_BIAS;
+            C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0[tt][tau], C, 0, 0, 0);
+            C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1[tt][tau], C, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                Ps[tt][g][v][lane] = biased_to_f32(C[v]);
+                Ss[tt][g][v][lane] = mul_f16_f32(swp[v >> 1], v & 1, xsv[tt][tau]);
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int tt = 0; tt < NTL; ++tt) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int g = 0; g < G; ++g) acc = __builtin_fmaf(Ss[tt][g][w][lane], Ps[tt][g][w][lane], acc);
+        const int t = t0 + 16 * tt + col;
+        if (t < a.dense_T) {
+            float* yp = a.Y + size_t(t) * a.R + 16 * s + 4 * q + w;
+            *yp = a.accumulate ? *yp + acc : acc;
+        }
+    }
+}
+
 template <int MODE, int NT>
 const void* kernel_ptr() { return reinterpret_cast<const void*>(&expert_gemm<MODE, NT>); }
 
@@ -540,7 +607,6 @@ hipError_t gemm_setup() {
         return e;
     if ((e = set_attr<GEMM_GATE_UP, 1>()) != hipSuccess) return e;
     if ((e = set_attr<GEMM_DOWN, 1>()) != hipSuccess) return e;
-    if ((e = set_attr<GEMM_DENSE, 1>()) != hipSuccess) return e;
     if ((e = set_attr<GEMM_PRODUCTS_GATE_UP, 4>()) != hipSuccess) return e;
     if ((e = set_attr<GEMM_PRODUCTS_DOWN, 4>()) != hipSuccess) return e;
     return hipSuccess;
@@ -563,12 +629,41 @@ hipError_t launch_expert_gemm_plan(const GemmArgs& a, const DecodePlanArgs& p, h
     return hipGetLastError();
 }
 
+template <int NTL>
+hipError_t dense_splitk_t(int bits, const GemmArgs& a, hipStream_t st) {
+    static bool attr = false;
+    if (!attr) {   // (above the default 64 KiB of LDS from two tiles on)
+        hipError_t e = hipSuccess;
+        for (const void* k : {reinterpret_cast<const void*>(&dense_splitk_kernel<2, NTL>),
+                              reinterpret_cast<const void*>(&dense_splitk_kernel<3, NTL>),
+                              reinterpret_cast<const void*>(&dense_splitk_kernel<4, NTL>),
+                              reinterpret_cast<const void*>(&dense_splitk_kernel<8, NTL>)})
+            if (e == hipSuccess) e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, dense_lds<NTL>());
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    const dim3 grid(a.R / 16, (a.dense_T + 16 * NTL - 1) / (16 * NTL));
+    constexpr int L = dense_lds<NTL>();
+    if (bits == 2) dense_splitk_kernel<2, NTL><<<grid, WAVES * 64, L, st>>>(a);
+    else if (bits == 3) dense_splitk_kernel<3, NTL><<<grid, WAVES * 64, L, st>>>(a);
+    else if (bits == 4) dense_splitk_kernel<4, NTL><<<grid, WAVES * 64, L, st>>>(a);
+    else if (bits == 8) dense_splitk_kernel<8, NTL><<<grid, WAVES * 64, L, st>>>(a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_dense_splitk(int bits, const GemmArgs& a, hipStream_t st) {
+    if (a.dense_T < 1 || a.dense_T > 32 || a.R % 16 || a.K != 2048) return hipErrorInvalidValue;
+    // one 16-token tile per workgroup: two tiles per workgroup (the strip read once for 32 tokens, half the
+    // workgroups, 66 KiB of LDS) measured 6.5 against 5.1 us at T = 32, [3072 x 2048]
+    return dense_splitk_t<1>(bits, a, st);
+}
+
 // mode: GemmMode; nt: 16-token tiles per work item, 1 for the layer GEMMs (experts with many tokens take the
 // tiled kernel), 4 for the products modes.
 hipError_t launch_expert_gemm(int mode, int nt, const GemmArgs& a, int max_items, hipStream_t st) {
     if (mode == GEMM_GATE_UP) return nt == 1 ? launch_t<GEMM_GATE_UP, 1>(a, max_items, st) : hipErrorInvalidValue;
     if (mode == GEMM_DOWN) return nt == 1 ? launch_t<GEMM_DOWN, 1>(a, max_items, st) : hipErrorInvalidValue;
-    if (mode == GEMM_DENSE) return nt == 1 ? launch_t<GEMM_DENSE, 1>(a, max_items, st) : hipErrorInvalidValue;
     if (mode == GEMM_PRODUCTS_GATE_UP) return launch_t<GEMM_PRODUCTS_GATE_UP, 4>(a, max_items, st);
     return launch_t<GEMM_PRODUCTS_DOWN, 4>(a, max_items, st);
 }

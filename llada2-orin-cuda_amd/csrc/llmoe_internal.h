@@ -351,8 +351,7 @@ struct GemmArgs {
     int32_t* P;                 // group-products out [n, R, K/128] (test entry)
     const int* tstart;          // tiled: [G + 1] first task of each workgroup (the work partition above)
     int accumulate;             // GEMM_DENSE: Y += acc instead of Y = acc
-    int dense_T;                // streamed GEMM_DENSE: the tokens, units computed in the kernel (items unused); 0: items
-    int dense_nrb;              // ... and the row blocks of the matrix (R / (16 GEMM_WAVES spw))
+    int dense_T;                // dense projection at T <= 32 (launch_dense_splitk): the tokens
     int fast;                   // gate_up: SiLU by the hardware exp / reciprocal and fp16 conversion
     // streamed down GEMM: with zin set, the B rows are staged as A8(FWHT-512(zin[slot])) instead of read from xq / xs /
     // xsum, and the units of row block 0 also write those rows to xq_out / xs_out / xsum_out
@@ -393,6 +392,8 @@ size_t packlib_matrix_bytes(int R, int K, int bits);
 
 hipError_t gemm_setup();   // function attributes (dynamic LDS), once per process
 hipError_t launch_expert_gemm(int mode, int nt, const GemmArgs& a, int max_items, hipStream_t st);
+// dense projection at T = a.dense_T <= 32 (K = 2048), split over K (one superblock per wave)
+hipError_t launch_dense_splitk(int bits, const GemmArgs& a, hipStream_t st);
 // the decode gate_up GEMM that builds the slot plan itself from the routing masks (a.items / a.n_items unused), and
 // writes the plan's lists (DecodePlanArgs::d) for the down GEMM and the combine
 struct DecodePlanArgs;
