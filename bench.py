@@ -128,19 +128,17 @@ def one_layer_config(llmoe, synth, torch, name, seed, T, mix, shared, pool, step
 
 
 def norm_step(llmoe, torch, Gs, x, steps, warmup):
-    """The layer step with the fused combine epilogue (llmoe_experts_norm): route, experts, combine + FWHT-2048
+    """The layer step with the fused combine epilogue (llmoe_layer_forward_norm): routing, experts, combine + FWHT-2048
     un-rotation + residual add + the next layer's RMSNorm / rotation / A8, cycling through the same layers."""
     T = x.shape[0]
     dev = x.device
-    xq, xs, xsum = llmoe.quantize_a8(x)
     signs = torch.from_numpy(np.where(np.random.default_rng(5).random(H) < 0.5, -1.0, 1.0).astype(np.float32)).to(dev)
     h = torch.randn((T, H), device=dev)
-    nxt = (torch.empty_like(xq), torch.empty_like(xs), torch.empty_like(xsum))
+    nxt = (torch.empty((T, H), dtype=torch.int8, device=dev), torch.empty((T, 16), dtype=torch.float32, device=dev),
+           torch.empty((T, 16), dtype=torch.int32, device=dev))
 
     def fn(i):
-        G = Gs[i % len(Gs)]
-        G.route(T, x=x)
-        G.experts_norm(xq, xs, xsum, signs, 1e-6, h, out=nxt)
+        Gs[i % len(Gs)].forward_norm(x, signs, 1e-6, h, out=nxt)
 
     dt = time_steps(fn, steps, warmup)
     comb = llmoe.time_stage_layers(Gs, "combine", 20)

@@ -30,6 +30,8 @@
  *                         next-layer RMSNorm / rotation / A8
  *   llmoe_layer_forward   the MoE half of Engine::layer_step / Engine::prefill (engine/engine.cu:445-479,
  *                         :616-649), without the norm/rotation before it and the un-rotation after it
+ *   llmoe_layer_forward_norm  the same with ops::moe_combine_norm's epilogue (engine/ops.cu:507-549): the MoE half
+ *                         of Engine::layer_step up to the next layer's A8 input
  */
 #ifndef LLMOE_H
 #define LLMOE_H
@@ -124,6 +126,14 @@ int llmoe_experts_scratch(llmoe_layer* layer, const int8_t* xq, const float* xs,
  * (llmoe_layer_buffers) are the same as route + experts. */
 int llmoe_layer_forward(llmoe_layer* layer, const float* x, const float* logits, int T, float* out,
                         llmoe_stream stream);
+
+/* llmoe_layer_forward with the epilogue of llmoe_experts_norm instead of writing out: route from x (or the given
+ * logits), the experts, then the combine, un-rotation, residual add into h, and the next layer's RMSNorm / rotation
+ * / A8 into q_next, s_next, sum_next (layouts as llmoe_experts_norm; hidden must be 2048). At decode the slot plan
+ * is built inside the gate_up GEMM, as in llmoe_layer_forward; same results as llmoe_route + llmoe_experts_norm. */
+int llmoe_layer_forward_norm(llmoe_layer* layer, const float* x, const float* logits, int T, const float* signs,
+                             float eps, float* h, int8_t* q_next, float* s_next, int32_t* sum_next,
+                             llmoe_stream stream);
 
 /* Numerics of a layer's expert stage (default LLMOE_NUMERICS_EXACT).
  *   EXACT: every stage follows one fixed fp32 operation sequence, so results are bit-identical run to run and to

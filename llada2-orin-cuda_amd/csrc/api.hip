@@ -630,6 +630,23 @@ int llmoe_layer_forward(llmoe_layer* L, const float* x, const float* logits, int
     return llmoe_experts(L, L->xq, L->xs, L->xsum, T, out, stream);
 }
 
+int llmoe_layer_forward_norm(llmoe_layer* L, const float* x, const float* logits, int T, const float* signs,
+                             float eps, float* h, int8_t* q_next, float* s_next, int32_t* sum_next,
+                             llmoe_stream stream) {
+    if (int rc = check_layer(L)) return rc;
+    if (int rc = check_T(L, T)) return rc;
+    if (!x || !signs || !h || !q_next || !s_next || !sum_next) return fail(LLMOE_EINVAL, "null argument");
+    if (L->d.hidden != 2048) return fail(LLMOE_EINVAL, "the rotation is FWHT-2048: hidden must be 2048");
+    if (L->d.top_k + (L->d.has_shared ? 1 : 0) > 9) return fail(LLMOE_EINVAL, "at most 9 slots per token");
+    if (!logits && !L->router_w) return fail(LLMOE_EINVAL, "layer created without a router matrix");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    // as llmoe_layer_forward: the A8 of x rides on the first routing kernel, the dispatch on the gate_up GEMM
+    if (int rc = route_impl(L, logits ? nullptr : x, logits, T, st, logits == nullptr, logits ? x : nullptr, true))
+        return rc;
+    return experts_impl(L, L->xq, L->xs, L->xsum, T, nullptr, NormOut{signs, eps, h, q_next, s_next, sum_next},
+                        layer_inter(L), st);
+}
+
 int llmoe_layer_set_numerics(llmoe_layer* L, int mode) {
     if (int rc = check_layer(L)) return rc;
     if (mode != LLMOE_NUMERICS_EXACT && mode != LLMOE_NUMERICS_FAST) return fail(LLMOE_EINVAL, "numerics mode %d", mode);

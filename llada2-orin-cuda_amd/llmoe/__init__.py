@@ -67,6 +67,7 @@ EXPORTS = [
     "llmoe_group_products", "llmoe_layer_set_profiling", "llmoe_layer_stage_ms", "llmoe_layer_time_stage", "llmoe_layers_time_stage",
     "llmoe_layer_load", "llmoe_model_signs", "llmoe_dense_create", "llmoe_dense_destroy", "llmoe_dense_forward",
     "llmoe_last_error", "llmoe_experts_scratch", "llmoe_layer_set_numerics", "llmoe_selftest_f16",
+    "llmoe_layer_forward_norm",
 ]
 
 STAGES = ["quant", "router", "route", "dispatch", "gate_up", "fwht", "down", "combine"]
@@ -100,6 +101,7 @@ def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.llmoe_experts_scratch.argtypes = [vp, vp, vp, vp, i, vp, vp]
     lib.llmoe_experts_norm.argtypes = [vp, vp, vp, vp, i, vp, f, vp, vp, vp, vp, vp]
     lib.llmoe_layer_forward.argtypes = [vp, vp, vp, i, vp, vp]
+    lib.llmoe_layer_forward_norm.argtypes = [vp, vp, vp, i, vp, f, vp, vp, vp, vp, vp]
     lib.llmoe_layer_buffers.argtypes = [vp, ctypes.POINTER(Buffers)]
     lib.llmoe_layer_weight_bytes.argtypes = [vp, ctypes.POINTER(sz)]
     lib.llmoe_group_products.argtypes = [vp, i, i, vp, vp, i, vp, vp]
@@ -232,6 +234,21 @@ class Layer:
         q, s, sm = out
         _check(self.lib.llmoe_experts_norm(self.handle, _ptr(xq), _ptr(xs), _ptr(xsum), T, _ptr(signs), float(eps),
                                            _ptr(h), _ptr(q), _ptr(s), _ptr(sm), _stream(stream)))
+        return q, s, sm
+
+    def forward_norm(self, x, signs, eps, h, logits=None, out=None, stream=None):
+        """The layer forward with the fused epilogue (llmoe_layer_forward_norm): h += the un-rotated MoE output (in
+        place); returns the next layer's A8 (q_next, s_next, sum_next), written into `out` when given."""
+        import torch
+        T = x.shape[0]
+        if out is None:
+            out = (torch.empty((T, 2048), dtype=torch.int8, device=x.device),
+                   torch.empty((T, 16), dtype=torch.float32, device=x.device),
+                   torch.empty((T, 16), dtype=torch.int32, device=x.device))
+        q, s, sm = out
+        _check(self.lib.llmoe_layer_forward_norm(self.handle, _ptr(x), _ptr(logits), T, _ptr(signs), float(eps),
+                                                 _ptr(h), _ptr(q), _ptr(s), _ptr(sm), _stream(stream)))
+        self.T = T
         return q, s, sm
 
     def group_products(self, expert: int, which: int, xq, xsum, stream=None):

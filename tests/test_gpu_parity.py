@@ -420,6 +420,39 @@ def test_experts_norm_bit_exact(gpu, T, pool):
     G.close()
 
 
+@pytest.mark.parametrize("T,pool,logits", [(32, 256, False), (32, 48, False), (5, 256, True), (200, 48, False)])
+def test_forward_norm_matches_route_experts_norm(gpu, T, pool, logits):
+    """llmoe_layer_forward_norm (at decode the self-planning gate_up) against llmoe_route + llmoe_experts_norm on the
+    same layer and inputs: h, q_next, s_next and sum_next bit for bit, on two consecutive calls."""
+    import torch
+    say(f"[forward_norm] T={T} pool={pool} logits={logits}")
+    L = layer_for("mixed", True)
+    G = make_gpu_layer(L, pool)
+    signs = to_dev(np.where(np.random.default_rng(5).random(2048) < 0.5, -1.0, 1.0).astype(np.float32), gpu)
+    for i in range(2):
+        x = to_dev(synth.make_x(3000 + 10 * T + i, T), gpu)
+        lg = to_dev(synth.logits_zipf(3100 + i, T), gpu) if logits else None
+        h0 = torch.randn((T, 2048), device=gpu)
+        h1 = h0.clone()
+        a = G.forward_norm(x, signs, 1e-6, h1, logits=lg)
+        torch.cuda.synchronize()
+        a = [t.clone() for t in a]
+        h2 = h0.clone()
+        if logits:
+            G.route(T, logits=lg)
+            xq, xs, xsum = (to_dev(v, gpu) for v in oracle.quant_a8(x.cpu().numpy()))
+        else:
+            G.route(T, x=x)
+            xq, xs, xsum = G.read("xq", (T, 2048), np.int8), G.read("xs", (T, 16), np.float32), G.read("xsum", (T, 16), np.int32)
+            xq, xs, xsum = to_dev(xq, gpu), to_dev(xs, gpu), to_dev(xsum, gpu)
+        b = G.experts_norm(xq, xs, xsum, signs, 1e-6, h2)
+        torch.cuda.synchronize()
+        assert torch.equal(h1.view(torch.int32), h2.view(torch.int32)), f"call {i}: h differs"
+        for name, u, v in zip(("q_next", "s_next", "sum_next"), a, b):
+            assert torch.equal(u.view(torch.uint8), v.view(torch.uint8)), f"call {i}: {name} differs"
+    G.close()
+
+
 def test_layer_load_matches_create(gpu, tmp_path):
     """llmoe_layer_load from a model directory in the reference's format == llmoe_layer_create on the same data."""
     say("[load] model dir")
