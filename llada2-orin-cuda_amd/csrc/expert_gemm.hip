@@ -135,9 +135,12 @@ template <int MODE, int NT>
 __host__ __device__ constexpr int ybuf_offset() {
     return b_bytes(16 * NT, Geo<MODE>::NSB * SB_K) + meta_bytes<MODE>() + 16 * NT * 4;   // + the B row table
 }
+// the gate_up GEMM's Z outputs of one unit (at most 16 tokens x 128 fp16)
+constexpr int ZBUF_BYTES = 16 * 128 * 2;
 template <int MODE, int NT>
 __host__ __device__ constexpr int lds_bytes() {
-    return ybuf_offset<MODE, NT>() + (MODE == GEMM_DOWN && NT == 1 ? YBUF_BYTES : 0);
+    return ybuf_offset<MODE, NT>() + (MODE == GEMM_DOWN && NT == 1 ? YBUF_BYTES : 0) +
+           (MODE == GEMM_GATE_UP && NT == 1 ? ZBUF_BYTES : 0);
 }
 
 // the plan of a self-planning decode gate_up GEMM: the unit's token rows come from its token masks
@@ -285,6 +288,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, con
     constexpr int UROWS = WAVES * SPW * 16;
     const bool ybuf = MODE == GEMM_DOWN && NT == 1 && ntok * UROWS * 4 <= YBUF_BYTES;
     float* ylds = reinterpret_cast<float*>(lds + ybuf_offset<MODE, NT>());
+    // gate_up: the same for Z ([slot][UROWS / 2] fp16), which always fits; the partial-wave Z stores inside the
+    // stream cost up to 0.67 us of the config-1 step (a diagnostic build without them)
+    constexpr bool ZBUF = MODE == GEMM_GATE_UP && NT == 1;
+    static_assert(!ZBUF || UROWS / 2 * 16 * 2 <= ZBUF_BYTES, "Z buffer");
+    uint32_t* zlds = reinterpret_cast<uint32_t*>(lds + ybuf_offset<MODE, NT>());
 
     // the wave's NSTEP superblocks (SPW strips of NSB each) are streamed as one ring (slot of step u = u % D). The steps are unrolled at compile time: across a loop back-edge the compiler would wait for every
     // outstanding load, and the prefetch would not overlap.
@@ -417,7 +425,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, con
                             z0 = f32_to_f16_rne(silu_f32(acc[nt][0]) * acc[nt][1]);
                             z1 = f32_to_f16_rne(silu_f32(acc[nt][2]) * acc[nt][3]);
                         }
-                        *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
+                        if constexpr (ZBUF) zlds[n * (UROWS / 4) + 4 * (strip - sbase) + q] = z0 | (z1 << 16);
+                        else *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
                     } else if (ybuf) {
                         *reinterpret_cast<float4*>(ylds + n * UROWS + 16 * (strip - sbase) + 4 * q) =
                             make_float4(wts[nt] * acc[nt][0], wts[nt] * acc[nt][1], wts[nt] * acc[nt][2],
@@ -434,6 +443,18 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const Item& it, con
         // refill the slot just consumed with step u + D
         if constexpr (u + D < NSTEP) load_step<BITS>(step_ptr(u + D), lane, cur);
     });
+    if constexpr (ZBUF) {
+        // the wave stores the Z it wrote (its strips j WAVES + wave, 16 bytes each per slot), one store per lane
+        // and no workgroup barrier (config 1: 0.0549 -> 0.0544 ms per step; through a barrier and a workgroup-wide
+        // pass: 0.0546)
+        static_assert(16 * Geo<MODE>::SPW_MAX <= 64, "one store per lane");
+        __builtin_amdgcn_wave_barrier();
+        if (lane < ntok * SPW) {
+            const int n = lane / SPW, c = (lane % SPW) * WAVES + wave;
+            *reinterpret_cast<uint4*>(a.Z + size_t(it.slot0 + n) * (a.R / 2) + 8 * (sbase + c)) =
+                *reinterpret_cast<const uint4*>(zlds + n * (UROWS / 4) + 4 * c);
+        }
+    }
     if constexpr (MODE == GEMM_DOWN && NT == 1) {
         if (ybuf) {
             __syncthreads();
