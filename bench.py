@@ -453,8 +453,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-headline", action="store_true", help="config 1 only (profiling runs)")
     ap.add_argument("--only-stack", action="store_true", help="config 3 only (profiling runs of the tiled GEMM)")
-    ap.add_argument("--only", choices=["config2", "config4-2", "config4-4", "config4-8"],
-                    help="one prefill configuration only, printed as its own JSON line (profiling runs)")
+    ap.add_argument("--only", choices=["config0", "config2", "config4-2", "config4-4", "config4-8"],
+                    help="one configuration only (config 0 or a prefill one), printed as its own JSON line "
+                         "(profiling runs)")
     ap.add_argument("--copy-calibration", action="store_true", help="run 512 MiB device copies first (counter runs)")
     ap.add_argument("--no-fast", action="store_true", help="exact numerics only (profiling runs of one kernel variant)")
     args = ap.parse_args()
@@ -475,7 +476,12 @@ def main():
         copy_calibration(torch)
 
     if args.only:
-        if args.only == "config2":
+        if args.only == "config0":
+            r, (_, G0s, _, _, _) = one_layer_config(llmoe, synth, torch, "config 0: 32 tokens, 4-bit, pool 48, "
+                                                    "no shared", 11, 32, 4, False, 48, args.steps, args.warmup)
+            for G in G0s:
+                G.close()
+        elif args.only == "config2":
             r = prefill_config(llmoe, synth, torch, "config 2", 512, "mixed", True, 48, None, *prefill_steps(args, 2),
                                nlayers=4, outliers=0.01)
         else:
