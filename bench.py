@@ -101,6 +101,12 @@ def one_layer_config(llmoe, synth, torch, name, seed, T, mix, shared, pool, step
     out = torch.empty((T, H), dtype=torch.float32, device=dev)
     fn = lambda i: Gs[i % nlayers].forward(x, out=out)  # noqa: E731
     dt = time_steps(fn, steps, warmup)
+    # a short window (the driver's --steps 20 --warmup 5) reads a GPU still ramping up: consecutive 20-step
+    # windows go from about 0.059 to 0.0557 ms over the first ten. The same steps re-timed after 300 more warm-up
+    # steps are reported beside the contract's figure (which stays the one above).
+    steady = None
+    if steps < 200 or warmup < 300:
+        steady = {"steps": 200, "warmup": 300, "ms_per_step": time_steps(fn, 200, 300) / 200 * 1e3}
     prof = stage_profile(Gs[0], lambda i: Gs[0].forward(x, out=out))
     for G in Gs:
         G.forward(x, out=out)
@@ -121,6 +127,8 @@ def one_layer_config(llmoe, synth, torch, name, seed, T, mix, shared, pool, step
         "int8_TOPS": 2 * slots * 3 * I * H / t_w / 1e12,
         "stage_ms": prof, "gate_up_bytes": gub, "down_bytes": dnb,
     }
+    if steady:
+        res["steady_state"] = steady
     res["fast_numerics"] = fast_numerics(llmoe, Gs, fn, steps, warmup, T)
     for G in Gs:
         G.forward(x, out=out)
@@ -553,6 +561,9 @@ def main():
         "roofline": roofline, "roofline_2048": roofline_2048(c3) if c3 else None, "cpu_baseline": cpu,
         "configs": configs,
     }
+    if "steady_state" in c1:   # short arguments: the same steps re-timed after 300 more warm-up steps (not `value`)
+        ss = c1["steady_state"]
+        line["steady_state"] = dict(ss, tokens_per_s=32 / (ss["ms_per_step"] * 1e-3))
     print(json.dumps(line))
 
 
