@@ -36,7 +36,13 @@ constexpr int GROUP_B = TILED_NTOK * GROUP;
 __host__ __device__ constexpr int lds_bytes_for(int K) {
     return (K / GROUP) * (GROUP_B + TILED_NTOK * 8) + TILED_NTOK * 4;
 }
-constexpr int LDS_BYTES = lds_bytes_for(2048);
+// gate_up with 8-bit codes: a row block's Z ([token][8 fp16 per strip of the row block], rows padded by 16 bytes so
+// that the 16 token columns of a store fall in different banks) goes through LDS and is stored as whole row segments
+__host__ __device__ constexpr int zbuf_pitch(int spw) { return 4 * tiled_waves(false) * spw + 4; }   // uint32
+constexpr int ZBUF_BYTES = TILED_NTOK * zbuf_pitch(1) * 4;
+__host__ __device__ constexpr int mode_lds_bytes(int mode) {
+    return mode == GEMM_DOWN ? lds_bytes_for(512) : lds_bytes_for(2048) + (mode == GEMM_GATE_UP ? ZBUF_BYTES : 0);
+}
 constexpr int NXCD = 8;   // XCDs of MI355X (accelerator complex dies, each with its own L2)
 
 template <int I, int N, class F>
@@ -391,7 +397,7 @@ __device__ __forceinline__ void rowblock_compute(const uint8_t* mat, const uint8
 // The row block's fused epilogue: Z = fp16(SiLU(g) u) (gate_up), Y = w acc (down) or Y (+)= acc (dense).
 template <int BITS, int MODE, int NTILE>
 __device__ __forceinline__ void rowblock_store(const GemmArgs& a, const Item& it, int rb,
-                                               const float (&acc)[RowRegs<BITS, MODE>::S][NTILE][4]) {
+                                               const float (&acc)[RowRegs<BITS, MODE>::S][NTILE][4], uint8_t* lds) {
     constexpr int S = RowRegs<BITS, MODE>::S, NW = nw_for(MODE == GEMM_DOWN ? SB_K : 4 * SB_K);
     const int lane = threadIdx.x & 63, q = lane >> 4, col = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -421,7 +427,11 @@ __device__ __forceinline__ void rowblock_store(const GemmArgs& a, const Item& it
                         z0 = f32_to_f16_rne(silu_f32(acc[s][nt][0]) * acc[s][nt][1]);
                         z1 = f32_to_f16_rne(silu_f32(acc[s][nt][2]) * acc[s][nt][3]);
                     }
-                    *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
+                    if constexpr (S == 1)
+                        reinterpret_cast<uint32_t*>(lds + lds_bytes_for(2048))[n * zbuf_pitch(S) + 4 * wave + q] =
+                            z0 | (z1 << 16);
+                    else
+                        *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
                 } else {
                     store_slot_out(a, size_t(slot) * a.R + 16 * strip + 4 * q, a.slot_weight[slot], acc[s][nt][0],
                                    acc[s][nt][1], acc[s][nt][2], acc[s][nt][3]);
@@ -447,7 +457,22 @@ __device__ __forceinline__ void tiled_body(const GemmArgs& a, const Item& it, co
         // registers together, so the stores go first)
         constexpr bool LOAD_FIRST = !(MODE == GEMM_DOWN && BITS == 8);
         if (LOAD_FIRST && rb + 1 < rb1) rowblock_load<BITS, MODE, NTILE>(mat, rb + 1, r);
-        rowblock_store<BITS, MODE, NTILE>(a, it, rb, acc);
+        // 8-bit codes (one strip per wave): the row block's Z goes through LDS and is stored as whole row segments
+        // (config-4 8-bit gate_up 0.264 -> 0.250 ms; for two strips per wave the two barriers cost what it saves)
+        constexpr bool ZSTAGE = MODE == GEMM_GATE_UP && RowRegs<BITS, MODE>::S == 1;
+        if constexpr (ZSTAGE) __syncthreads();   // the previous row block's Z has been read
+        rowblock_store<BITS, MODE, NTILE>(a, it, rb, acc, lds);
+        if constexpr (ZSTAGE) {
+            __syncthreads();
+            // each token's 8 NW Z values of the row block are contiguous in Z: 16 bytes (one strip) per thread
+            constexpr int S = RowRegs<BITS, MODE>::S, NCH = S * tiled_waves(false);
+            const uint32_t* zb = reinterpret_cast<const uint32_t*>(lds + lds_bytes_for(2048));
+            for (int idx = threadIdx.x; idx < it.ntok * NCH; idx += nthreads_for(K)) {
+                const int n = idx / NCH, c = idx % NCH;
+                *reinterpret_cast<uint4*>(a.Z + size_t(it.slot0 + n) * (a.R / 2) + 8 * (rb * NCH + c)) =
+                    *reinterpret_cast<const uint4*>(zb + n * zbuf_pitch(S) + 4 * c);
+            }
+        }
         if (!LOAD_FIRST && rb + 1 < rb1) rowblock_load<BITS, MODE, NTILE>(mat, rb + 1, r);
     }
 }
@@ -518,7 +543,7 @@ int grid_t() {
         if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (e == hipSuccess)
             e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kptr<MODE>(), nthreads_for(MODE == GEMM_DOWN ? 512 : 2048),
-                                                             lds_bytes_for(MODE == GEMM_DOWN ? 512 : 2048));
+                                                             mode_lds_bytes(MODE));
         if (e != hipSuccess) return 0;
         grid = cus * (per_cu > 0 ? per_cu : 1);
     }
@@ -530,16 +555,19 @@ hipError_t launch_t(const GemmArgs& a, hipStream_t st) {
     const int grid = grid_t<MODE>();
     if (!grid) return hipErrorInvalidDevice;
     constexpr int K = MODE == GEMM_DOWN ? 512 : 2048;
-    tiled_gemm<MODE><<<grid, nthreads_for(K), lds_bytes_for(K), st>>>(a);
+    tiled_gemm<MODE><<<grid, nthreads_for(K), mode_lds_bytes(MODE), st>>>(a);
     return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t tiled_setup() {
-    hipError_t e = hipFuncSetAttribute(kptr<GEMM_GATE_UP>(), hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
-    if (e == hipSuccess) e = hipFuncSetAttribute(kptr<GEMM_DOWN>(), hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
-    if (e == hipSuccess) e = hipFuncSetAttribute(kptr<GEMM_DENSE>(), hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+    hipError_t e = hipFuncSetAttribute(kptr<GEMM_GATE_UP>(), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       mode_lds_bytes(GEMM_GATE_UP));
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(kptr<GEMM_DOWN>(), hipFuncAttributeMaxDynamicSharedMemorySize, mode_lds_bytes(GEMM_DOWN));
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(kptr<GEMM_DENSE>(), hipFuncAttributeMaxDynamicSharedMemorySize, mode_lds_bytes(GEMM_DENSE));
     return e;
 }
 
