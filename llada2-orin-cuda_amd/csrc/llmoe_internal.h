@@ -368,6 +368,19 @@ struct GemmArgs {
 
 // The down GEMM's slot outputs w acc of one lane (4 consecutive rows from element index i): fp32 into Y, or, with
 // fast numerics, rounded to fp16 (nearest even) into Yh
+// Stores that every lane issues: a lane whose `ok` is false writes nothing (its byte offset is moved past the
+// buffer's 2^31 - 1 byte range, and the hardware drops an out-of-range buffer store). A store inside a divergent
+// branch may or may not have been issued, so the compiler's waits for later loads must also wait for it; these do
+// not. `base` must be the same for the whole wave (scalar values only), offsets below 2^31.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t store_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ uint32_t store_off(uint32_t byte_off, bool ok) {
+    return byte_off + (uint32_t(!ok) << 31);
+}
+__device__ __forceinline__ void store_b32_if(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, bool ok, uint32_t v) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, store_off(byte_off, ok), 0, 0);
+}
 __device__ __forceinline__ void store_slot_out(const GemmArgs& a, size_t i, float w, float a0, float a1, float a2,
                                                float a3) {
     if (a.Yh) {

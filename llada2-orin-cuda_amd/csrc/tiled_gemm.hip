@@ -394,7 +394,10 @@ __device__ __forceinline__ void rowblock_compute(const uint8_t* mat, const uint8
 
 }
 
-// The row block's fused epilogue: Z = fp16(SiLU(g) u) (gate_up), Y = w acc (down) or Y (+)= acc (dense).
+// The row block's fused epilogue: Z = fp16(SiLU(g) u) (gate_up), Y = w acc (down) or Y (+)= acc (dense). The Z
+// stores are issued by every lane (absent tokens' stores dropped), so that the waits for the next row block's weights
+// need not wait for them: the loop head then waits with vmcnt(10) instead of vmcnt(2) (2-bit, 4 token tiles; config 3
+// gate_up -1 %).
 template <int BITS, int MODE, int NTILE>
 __device__ __forceinline__ void rowblock_store(const GemmArgs& a, const Item& it, int rb,
                                                const float (&acc)[RowRegs<BITS, MODE>::S][NTILE][4], uint8_t* lds) {
@@ -402,40 +405,46 @@ __device__ __forceinline__ void rowblock_store(const GemmArgs& a, const Item& it
     const int lane = threadIdx.x & 63, q = lane >> 4, col = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int strip0 = (rb * NW + wave) * S;
+    // the chunk's rows of Z (slot0 is the same for the whole workgroup)
+    const __amdgpu_buffer_rsrc_t rz = store_rsrc(a.Z + size_t(it.slot0) * (a.R / 2));
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int strip = strip0 + s;
 #pragma unroll
         for (int nt = 0; nt < NTILE; ++nt) {
             const int n = nt * 16 + col;
-            if (n < it.ntok) {
-                const int slot = it.slot0 + n;
-                if constexpr (MODE == GEMM_DENSE) {
-                    float4* yp = reinterpret_cast<float4*>(a.Y + size_t(slot) * a.R + 16 * strip + 4 * q);
+            const bool ok = n < it.ntok;
+            if constexpr (MODE == GEMM_DENSE) {
+                if (ok) {
+                    float4* yp = reinterpret_cast<float4*>(a.Y + size_t(it.slot0 + n) * a.R + 16 * strip + 4 * q);
                     float4 y = make_float4(acc[s][nt][0], acc[s][nt][1], acc[s][nt][2], acc[s][nt][3]);
                     if (a.accumulate) {
                         const float4 o = *yp;
                         y = make_float4(o.x + y.x, o.y + y.y, o.z + y.z, o.w + y.w);
                     }
                     *yp = y;
-                } else if constexpr (MODE == GEMM_GATE_UP) {
-                    uint32_t z0, z1;
-                    if (a.fast) {
-                        z0 = silu_mul_f16_fast(acc[s][nt][0], acc[s][nt][1]);
-                        z1 = silu_mul_f16_fast(acc[s][nt][2], acc[s][nt][3]);
-                    } else {
-                        z0 = f32_to_f16_rne(silu_f32(acc[s][nt][0]) * acc[s][nt][1]);
-                        z1 = f32_to_f16_rne(silu_f32(acc[s][nt][2]) * acc[s][nt][3]);
-                    }
-                    if constexpr (S == 1)
+                }
+            } else if constexpr (MODE == GEMM_GATE_UP) {
+                uint32_t z0, z1;
+                if (a.fast) {
+                    z0 = silu_mul_f16_fast(acc[s][nt][0], acc[s][nt][1]);
+                    z1 = silu_mul_f16_fast(acc[s][nt][2], acc[s][nt][3]);
+                } else {
+                    z0 = f32_to_f16_rne(silu_f32(acc[s][nt][0]) * acc[s][nt][1]);
+                    z1 = f32_to_f16_rne(silu_f32(acc[s][nt][2]) * acc[s][nt][3]);
+                }
+                if constexpr (S == 1) {
+                    if (ok)
                         reinterpret_cast<uint32_t*>(lds + lds_bytes_for(2048))[n * zbuf_pitch(S) + 4 * wave + q] =
                             z0 | (z1 << 16);
-                    else
-                        *reinterpret_cast<uint32_t*>(a.Z + size_t(slot) * (a.R / 2) + 8 * strip + 2 * q) = z0 | (z1 << 16);
                 } else {
-                    store_slot_out(a, size_t(slot) * a.R + 16 * strip + 4 * q, a.slot_weight[slot], acc[s][nt][0],
-                                   acc[s][nt][1], acc[s][nt][2], acc[s][nt][3]);
+                    store_b32_if(rz, uint32_t(n * (a.R / 2) + 8 * strip + 2 * q) * 2u, ok, z0 | (z1 << 16));
                 }
+            } else {
+                // (unconditional stores here need 24 bytes of spills at the down kernel's 128 VGPRs)
+                if (ok)
+                    store_slot_out(a, size_t(it.slot0 + n) * a.R + 16 * strip + 4 * q, a.slot_weight[it.slot0 + n],
+                                   acc[s][nt][0], acc[s][nt][1], acc[s][nt][2], acc[s][nt][3]);
             }
         }
     }
