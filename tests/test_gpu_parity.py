@@ -351,6 +351,37 @@ def test_tiled_units_bit_exact(gpu, T, mix, kind):
     G.close()
 
 
+def test_tiled_absent_token_stores_dropped(gpu):
+    """The tiled gate_up issues its Z stores (2/3/4-bit codes) from every lane and relies on the buffer range check
+    to drop those of absent tokens (rows slot0 + n, n >= ntok, of a chunk). All-2-bit layer without the shared
+    expert, T = 100, logits that put every token on the last expert: its 100 slots are the last of the layer, split
+    into tiled chunks, so a store of an absent token that was not dropped would land in the rows past the last
+    slot. Those rows of the workspace, filled with a sentinel first, must keep it; Z and the output stay
+    bit-exact."""
+    import ctypes
+    T, Tmax, E = 100, 160, 256
+    say(f"[tiled stores] T={T} max_tokens={Tmax}")
+    L = layer_for(2, False, seed=62)
+    lg = synth.logits_zipf(T + 3, T)
+    lg[:, E - 1] += 100.0                      # every token's first choice
+    G = make_gpu_layer(L, 256, max_tokens=Tmax)
+    rows = Tmax * 9
+    sentinel = np.full((rows, 512), 0x7E7E, np.uint16)
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert hip.hipMemcpy(G.buffers().Z, sentinel.ctypes.data, sentinel.nbytes, 1) == 0   # host to device
+    x = synth.make_x(700, T)
+    out = run_layer(G, x, gpu, logits=lg)
+    S = T * 8
+    Z = G.read("Z", (rows, 512), np.uint16)
+    r = oracle.Layer(L).forward(x, logits=lg, C=256)
+    assert r["count"][E - 1] == T, "every token must pick the last expert"
+    assert (Z[S:] == 0x7E7E).all(), "a store of an absent token reached the rows past the last slot"
+    assert np.array_equal(Z[:S], r["Z"]), "Z not bit-exact"
+    assert np.array_equal(out.view(np.uint32), r["out"].view(np.uint32)), "combine not bit-exact"
+    G.close()
+
+
 @pytest.mark.parametrize("T,mix,shared,pool,kind", [
     (512, "mixed", True, 48, None),       # config 2: router x Wr with outlier channels, block pool 48
     (2048, "mixed", True, 256, "zipf"),   # one layer of config 3
