@@ -406,7 +406,8 @@ __device__ __forceinline__ void rowblock_store(const GemmArgs& a, const Item& it
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int strip0 = (rb * NW + wave) * S;
     // the chunk's rows of Z (slot0 is the same for the whole workgroup)
-    const __amdgpu_buffer_rsrc_t rz = store_rsrc(a.Z + size_t(it.slot0) * (a.R / 2));
+    const __amdgpu_buffer_rsrc_t rz =
+        store_rsrc(MODE == GEMM_GATE_UP ? static_cast<const void*>(a.Z + size_t(it.slot0) * (a.R / 2)) : nullptr);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int strip = strip0 + s;
