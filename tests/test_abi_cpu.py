@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import llmoe
+from llmoe import synth
 
 ROOT = Path(__file__).resolve().parents[1]
 
@@ -44,9 +45,9 @@ def _create(desc_kw, bits=None, blob_bytes=None):
         setattr(d, k, v)
     E = d.n_experts + d.has_shared
     bits = np.full(max(E, 1), 2, np.int8) if bits is None else bits
-    eb = llmoe.synth.expert_bytes(2)
+    eb = synth.expert_bytes(2)
     gu = np.arange(max(E, 1), dtype=np.uint64) * np.uint64(eb)
-    dd = gu + np.uint64(llmoe.synth.matrix_bytes(1024, 2048, 2))
+    dd = gu + np.uint64(synth.matrix_bytes(1024, 2048, 2))
     blob = np.zeros(16, np.uint8)
     nbytes = eb * E if blob_bytes is None else blob_bytes
     bias = np.zeros(max(E, 1), np.float32)
@@ -88,8 +89,8 @@ def test_load_missing_dir(lib, tmp_path):
 
 
 def test_load_rejects_bad_index(lib, tmp_path):
-    L = llmoe.synth.make_layer(3, E=64, experts=[0], shared=True)
-    llmoe.synth.write_model_dir(tmp_path, L, li=2)
+    L = synth.make_layer(3, E=64, experts=[0], shared=True)
+    synth.write_model_dir(tmp_path, L, li=2)
     idx = (tmp_path / "engine.idx").read_text()
     rc, err = _load(tmp_path, layer=5)
     assert rc == llmoe.LLMOE_EINVAL and "layer 5" in err
@@ -105,8 +106,8 @@ def test_load_rejects_bad_index(lib, tmp_path):
 
 
 def test_model_signs(lib, tmp_path):
-    L = llmoe.synth.make_layer(4, E=64, experts=[0], shared=True)
-    ref = llmoe.synth.write_model_dir(tmp_path, L, li=1)
+    L = synth.make_layer(4, E=64, experts=[0], shared=True)
+    ref = synth.write_model_dir(tmp_path, L, li=1)
     out = np.zeros(2048, np.float32)
     assert llmoe.load_library().llmoe_model_signs(str(tmp_path).encode(), out.ctypes.data, 2048) == 0
     np.testing.assert_array_equal(out, ref["signs"])
@@ -121,3 +122,28 @@ def test_dense_create_rejects(lib):
         assert rc == llmoe.LLMOE_EINVAL, (rows, k, bits)
     rc = lib.llmoe_dense_create(512, 2048, 8, blob.ctypes.data, blob.nbytes, 32, ctypes.byref(h))
     assert rc == llmoe.LLMOE_EINVAL and "blob" in lib.llmoe_last_error().decode()
+
+
+# every entry point that takes a layer, called with a null one: LLMOE_EINVAL and a message, no device call
+_NULL_LAYER_CALLS = {
+    "llmoe_route": lambda f: f(None, None, None, 32, None),
+    "llmoe_dispatch": lambda f: f(None, None, None, 32, None),
+    "llmoe_experts": lambda f: f(None, None, None, None, 32, None, None),
+    "llmoe_experts_norm": lambda f: f(None, None, None, None, 32, None, ctypes.c_float(1e-6), None, None, None, None,
+                                      None),
+    "llmoe_experts_scratch": lambda f: f(None, None, None, None, 32, None, None),
+    "llmoe_layer_forward": lambda f: f(None, None, None, 32, None, None),
+    "llmoe_layer_forward_norm": lambda f: f(None, None, None, 32, None, ctypes.c_float(1e-6), None, None, None, None,
+                                            None),
+    "llmoe_layer_set_numerics": lambda f: f(None, 0),
+    "llmoe_layer_set_profiling": lambda f: f(None, 1),
+    "llmoe_layer_buffers": lambda f: f(None, ctypes.byref(llmoe.Buffers())),
+    "llmoe_layer_weight_bytes": lambda f: f(None, ctypes.byref(ctypes.c_size_t())),
+}
+
+
+@pytest.mark.parametrize("name", sorted(_NULL_LAYER_CALLS))
+def test_null_layer_rejected(lib, name):
+    rc = _NULL_LAYER_CALLS[name](getattr(lib, name))
+    assert rc == -1, f"{name} returned {rc}"   # LLMOE_EINVAL
+    assert b"null layer" in lib.llmoe_last_error(), lib.llmoe_last_error()
