@@ -441,14 +441,16 @@ def cpu_baseline(L, x_np, pool, seconds):
 
 
 def prefill_steps(args, config):
-    """(timed steps, warm-up steps) of a prefill configuration: a share of --steps / --warmup with a floor, so that
+    """(timed steps, warm-up steps) of a prefill configuration: a share of --steps / --warmup with floors, so that
     the 2048- and 4096-token half of the metric is never timed from one or two steps (config 3 is a 20-layer stack
-    of ~5 ms per step, config 4 one layer of ~0.4-0.6 ms, config 2 one layer of ~0.13 ms)."""
+    of ~5 ms per step, config 4 one layer of ~0.4-0.6 ms, config 2 one layer of ~0.13 ms), nor right after the
+    layers are built: the warm-up is at least ~15 ms of GPU work (the GPU takes ~10-15 ms of steady work to reach its
+    steady step time)."""
     if config == 3:
-        return max(5, args.steps // 20), max(2, args.warmup // 10)
+        return max(5, args.steps // 20), max(3, args.warmup // 10)
     if config == 4:
-        return max(10, args.steps // 20), max(3, args.warmup // 20)
-    return max(20, args.steps // 5), max(5, args.warmup // 10)
+        return max(10, args.steps // 20), max(40, args.warmup // 20)
+    return max(20, args.steps // 5), max(100, args.warmup // 3)
 
 
 def main():
@@ -526,7 +528,9 @@ def main():
         configs.append(c3)
         for T in (32, 2048):
             log(f"[bench] dense projection, {T} tokens")
-            configs.append(dense_config(llmoe, synth, torch, 3072, 8, T, max(5, args.steps // 4), 5))
+            # (warm-up: ~15 ms of calls, as for the prefill configurations)
+            configs.append(dense_config(llmoe, synth, torch, 3072, 8, T, max(5, args.steps // 4),
+                                        2000 if T <= 32 else 400))
         for bits in (2, 4, 8):
             for kind in ("uniform", "skewed"):
                 log(f"[bench] config 4: {bits}-bit {kind}")
