@@ -176,6 +176,9 @@ def check_full(G, r, T, K, shared, tokens=None):
     (45, "mixed", True, 48),     # ragged last block
     (96, 8, True, 256),
     (200, "mixed", True, 48),    # tiled units for the shared expert and the pool's busiest experts
+    (33, "mixed", True, 256),    # the first T over one routing block: a second block of one token
+    (64, 2, False, 48),          # exactly two blocks
+    (256, "mixed", True, 256),   # T = the layer's max_tokens
 ])
 def test_layer_forward_matches_oracle(gpu, T, mix, shared, pool):
     say(f"[layer] T={T} mix={mix} shared={shared} pool={pool}")
