@@ -14,8 +14,8 @@ constexpr int MAXB_BLOCKS = 128;       // routing blocks whose masks the planner
 
 // logits partial c: fma chain over k = c H/8 .. (c+1) H/8 - 1 ascending from 0 (the summation order is fixed so
 // the CPU checker reproduces it). Workgroup tile: TT tokens x EW experts of one K chunk, the chunk's x slice and
-// its Wr slice (transposed, k contiguous per expert) staged in LDS by one batch of loads; each thread runs one
-// chain per (token, expert) it owns. grid (E/EW, ceil(T/TT), 8).
+// its Wr slice (transposed, k contiguous per expert) staged in LDS, KS of k at a time; each thread runs one chain
+// per (token, expert) it owns. grid (E/EW, ceil(T/TT), 8).
 // With q != nullptr the workgroups also write the A8 of the x slice (two 128-groups per token, the same operations
 // as quant_a8_kernel, spread over the expert slices), so the layer input is quantised without a launch of its own.
 __device__ __forceinline__ uint32_t okey(float v) {        // order-preserving unsigned image of a float
@@ -24,51 +24,32 @@ __device__ __forceinline__ uint32_t okey(float v) {        // order-preserving u
 }
 
 constexpr int RKW = 256;                                          // K per chunk (H = 2048)
-constexpr int RXS = RKW + 4;                                      // LDS row stride of the x and Wr slices
-template <int TT, int EW>
-constexpr int router_lds() { return (TT + EW) * RXS * 4; }
+template <int KS>
+constexpr int router_stride() { return KS + 4; }                  // LDS row stride of the x and Wr slices
+template <int TT, int EW, int KS>
+constexpr int router_lds() { return (TT + EW) * router_stride<KS>() * 4; }
 // Tiles: <32 tokens, 8 experts, 256 threads> (one chain per thread: the decode step, latency-bound) and
-// <64 tokens, 64 experts, 512 threads> (2 tokens x 4 experts per thread: x and Wr reloaded 8x less from L2).
-template <int TT, int EW, int NT>
+// <64 tokens, 64 experts, 512 threads> (2 tokens x 4 experts per thread: x and Wr reloaded 8x less from L2). The
+// chunk's K is staged KS at a time (the chains continue across the sub-chunks, so the order is the chunk's k
+// ascending either way): KS = 128 keeps the large tile's LDS at 66 KiB, two workgroups per CU (at 512 tokens
+// 20.0 -> 19.4 us per router stage, at 2048 tokens 66 -> 53 us, against one 133 KiB stage of 256 k). 4 tokens x 4
+// experts per thread (half the LDS reads per fma, one wave per SIMD) measured 23 us at 512 tokens.
+template <int TT, int EW, int NT, int TPT, int KS>
 __global__ void __launch_bounds__(NT) router_logits_kernel(const float* __restrict__ x, const float* __restrict__ Wr,
                                                            int T, int H, int E, float* __restrict__ part,
                                                            int8_t* __restrict__ q, float* __restrict__ qs,
                                                            int* __restrict__ qsum) {
-    constexpr int TPT = TT * EW / NT >= 8 ? 2 : 1, EPT = TT * EW / NT / TPT;   // chains per thread: TPT x EPT
-    constexpr int EG = EW / EPT;                                             // expert groups (threads per token group)
-    constexpr int XV = TT * (RKW / 4) / NT, WV = RKW * (EW / 4) / NT;
-    static_assert(XV * NT == TT * (RKW / 4) && WV * NT == RKW * (EW / 4) && NT >= TT * 8, "router tile");
+    constexpr int EPT = TT * EW / NT / TPT;                      // chains per thread: TPT x EPT
+    constexpr int EG = EW / EPT;                                 // expert groups (threads per token group)
+    constexpr int RS = router_stride<KS>(), K4 = KS / 4;
+    constexpr int XV = TT * K4 / NT, WV = KS * (EW / 4) / NT;
+    static_assert(XV * NT == TT * K4 && WV * NT == KS * (EW / 4) && TPT * EPT * NT == TT * EW && RKW % KS == 0 &&
+                  KS % 128 == 0, "router tile");
     extern __shared__ __align__(16) float rl[];
-    float* xs = rl;                       // [TT][RXS]
-    float* ws = rl + TT * RXS;            // [EW][RXS]: Wr slice transposed, k contiguous per expert
-    const int e0 = blockIdx.x * EW, t0 = blockIdx.y * TT, c = blockIdx.z, kb = c * RKW;
+    float* xs = rl;                       // [TT][RS]
+    float* ws = rl + TT * RS;             // [EW][RS]: Wr slice transposed, k contiguous per expert
+    const int e0 = blockIdx.x * EW, t0 = blockIdx.y * TT, c = blockIdx.z;
     const int tid = threadIdx.x;
-    float4 xv[XV], wv[WV];
-#pragma unroll
-    for (int i = 0; i < XV; ++i) {                                // x: TT x 256 floats as float4
-        const int idx = tid + NT * i, t = idx >> 6, k4 = idx & 63;
-        xv[i] = t0 + t < T ? *reinterpret_cast<const float4*>(x + size_t(t0 + t) * H + kb + 4 * k4)
-                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
-#pragma unroll
-    for (int i = 0; i < WV; ++i) {                                // Wr: 256 x EW floats as float4
-        const int idx = tid + NT * i, k = idx / (EW / 4), e4 = idx % (EW / 4);
-        wv[i] = *reinterpret_cast<const float4*>(Wr + size_t(kb + k) * E + e0 + 4 * e4);
-    }
-#pragma unroll
-    for (int i = 0; i < XV; ++i) {
-        const int idx = tid + NT * i, t = idx >> 6, k4 = idx & 63;
-        *reinterpret_cast<float4*>(xs + t * RXS + 4 * k4) = xv[i];
-    }
-#pragma unroll
-    for (int i = 0; i < WV; ++i) {
-        const int idx = tid + NT * i, k = idx / (EW / 4), e4 = idx % (EW / 4);
-        ws[(4 * e4 + 0) * RXS + k] = wv[i].x;
-        ws[(4 * e4 + 1) * RXS + k] = wv[i].y;
-        ws[(4 * e4 + 2) * RXS + k] = wv[i].z;
-        ws[(4 * e4 + 3) * RXS + k] = wv[i].w;
-    }
-    __syncthreads();
     // thread (token group tg, expert group eg): tokens tg TPT + i, experts j EG + eg (consecutive rows of the Wr
     // slice across a wave's lanes: conflict-free), one fma chain each over the chunk's k ascending
     const int tg = tid / EG, eg = tid % EG;
@@ -77,22 +58,68 @@ __global__ void __launch_bounds__(NT) router_logits_kernel(const float* __restri
     for (int i = 0; i < TPT; ++i)
 #pragma unroll
         for (int j = 0; j < EPT; ++j) acc[i][j] = 0.0f;
+    for (int h = 0; h < RKW / KS; ++h) {
+        const int kb = c * RKW + h * KS;
+        float4 xv[XV], wv[WV];
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {                            // x: TT x KS floats as float4
+            const int idx = tid + NT * i, t = idx / K4, k4 = idx % K4;
+            xv[i] = t0 + t < T ? *reinterpret_cast<const float4*>(x + size_t(t0 + t) * H + kb + 4 * k4)
+                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int i = 0; i < WV; ++i) {                            // Wr: KS x EW floats as float4
+            const int idx = tid + NT * i, k = idx / (EW / 4), e4 = idx % (EW / 4);
+            wv[i] = *reinterpret_cast<const float4*>(Wr + size_t(kb + k) * E + e0 + 4 * e4);
+        }
+        if (h > 0) __syncthreads();                               // the previous sub-chunk has been read
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            const int idx = tid + NT * i, t = idx / K4, k4 = idx % K4;
+            *reinterpret_cast<float4*>(xs + t * RS + 4 * k4) = xv[i];
+        }
+#pragma unroll
+        for (int i = 0; i < WV; ++i) {
+            const int idx = tid + NT * i, k = idx / (EW / 4), e4 = idx % (EW / 4);
+            ws[(4 * e4 + 0) * RS + k] = wv[i].x;
+            ws[(4 * e4 + 1) * RS + k] = wv[i].y;
+            ws[(4 * e4 + 2) * RS + k] = wv[i].z;
+            ws[(4 * e4 + 3) * RS + k] = wv[i].w;
+        }
+        __syncthreads();
 #pragma unroll 4
-    for (int k = 0; k < RKW; k += 4) {
-        float4 a[TPT], b[EPT];
+        for (int k = 0; k < KS; k += 4) {
+            float4 a[TPT], b[EPT];
 #pragma unroll
-        for (int i = 0; i < TPT; ++i) a[i] = *reinterpret_cast<const float4*>(xs + (tg * TPT + i) * RXS + k);
+            for (int i = 0; i < TPT; ++i) a[i] = *reinterpret_cast<const float4*>(xs + (tg * TPT + i) * RS + k);
 #pragma unroll
-        for (int j = 0; j < EPT; ++j) b[j] = *reinterpret_cast<const float4*>(ws + (j * EG + eg) * RXS + k);
+            for (int j = 0; j < EPT; ++j) b[j] = *reinterpret_cast<const float4*>(ws + (j * EG + eg) * RS + k);
 #pragma unroll
-        for (int i = 0; i < TPT; ++i)
+            for (int i = 0; i < TPT; ++i)
 #pragma unroll
-            for (int j = 0; j < EPT; ++j) {
-                acc[i][j] = __builtin_fmaf(a[i].x, b[j].x, acc[i][j]);
-                acc[i][j] = __builtin_fmaf(a[i].y, b[j].y, acc[i][j]);
-                acc[i][j] = __builtin_fmaf(a[i].z, b[j].z, acc[i][j]);
-                acc[i][j] = __builtin_fmaf(a[i].w, b[j].w, acc[i][j]);
+                for (int j = 0; j < EPT; ++j) {
+                    acc[i][j] = __builtin_fmaf(a[i].x, b[j].x, acc[i][j]);
+                    acc[i][j] = __builtin_fmaf(a[i].y, b[j].y, acc[i][j]);
+                    acc[i][j] = __builtin_fmaf(a[i].z, b[j].z, acc[i][j]);
+                    acc[i][j] = __builtin_fmaf(a[i].w, b[j].w, acc[i][j]);
+                }
+        }
+        if (q != nullptr) {
+            // A8 of the sub-chunk's x slice (KS / 128 groups per token): LPT = KS / 8 lanes per token, 8 values each,
+            // 64 / LPT tokens per wave job; wave w of expert slice b takes jobs w E/EW + b + i NWV E/EW, so the jobs
+            // are spread over the expert slices' workgroups
+            constexpr int NWV = NT / 64, LPT = KS / 8, TPW = 64 / LPT;
+            const int lane = tid & 63;
+            for (int j = (tid >> 6) * int(gridDim.x) + int(blockIdx.x); j < TT / TPW; j += NWV * int(gridDim.x)) {
+                const int tt = TPW * j + lane / LPT, l = lane % LPT;
+                const float4 a = *reinterpret_cast<const float4*>(xs + tt * RS + 8 * l);
+                const float4 b = *reinterpret_cast<const float4*>(xs + tt * RS + 8 * l + 4);
+                const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                const int t = t0 + tt;   // (rows beyond T: computed on zeros, not written)
+                const size_t gi = size_t(t) * (H / GROUP) + kb / GROUP + (l >> 4);
+                quant_a8_8(v, lane, q + size_t(t) * H + kb + 8 * l, qs + gi, qsum + gi, t < T);
             }
+        }
     }
 #pragma unroll
     for (int i = 0; i < TPT; ++i) {
@@ -100,22 +127,6 @@ __global__ void __launch_bounds__(NT) router_logits_kernel(const float* __restri
         if (t < T)
 #pragma unroll
             for (int j = 0; j < EPT; ++j) part[(size_t(c) * T + t) * E + e0 + j * EG + eg] = acc[i][j];
-    }
-    if (q != nullptr) {
-        // A8 of the chunk's x slice (two 128-groups per token), one pair of tokens per wave: lanes 0-31 the first
-        // token, 32-63 the second, 8 values each; wave w of expert slice b takes job w E/EW + b, so the jobs fall
-        // on different workgroups and no workgroup adds more than one job to its logits
-        constexpr int NWV = NT / 64;
-        const int lane = tid & 63;
-        for (int j = (tid >> 6) * int(gridDim.x) + int(blockIdx.x); j < TT / 2; j += NWV * int(gridDim.x)) {
-            const int tt = 2 * j + (lane >> 5), l = lane & 31;
-            const float4 a = *reinterpret_cast<const float4*>(xs + tt * RXS + 8 * l);
-            const float4 b = *reinterpret_cast<const float4*>(xs + tt * RXS + 8 * l + 4);
-            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-            const int t = t0 + tt;   // (rows beyond T: computed on zeros, not written)
-            const size_t gi = size_t(t) * (H / GROUP) + c * (RKW / GROUP) + (l >> 4);
-            quant_a8_8(v, lane, q + size_t(t) * H + kb + 8 * l, qs + gi, qsum + gi, t < T);
-        }
     }
 }
 
@@ -643,21 +654,22 @@ hipError_t launch_router_logits(const float* x, const float* Wr, int T, int H, i
                                 float* qs, int* qsum, hipStream_t st) {
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(router_logits_kernel<32, 8, 256>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, router_lds<32, 8>());
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(router_logits_kernel<32, 8, 256, 1, 256>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, router_lds<32, 8, 256>());
         if (e == hipSuccess)
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(router_logits_kernel<64, 64, 512>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, router_lds<64, 64>());
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(router_logits_kernel<64, 64, 512, 2, 128>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, router_lds<64, 64, 128>());
         if (e != hipSuccess) return e;
         attr = true;
     }
     if (T <= 32) {
         const dim3 grid(E / 8, 1, ROUTER_KC);
-        router_logits_kernel<32, 8, 256><<<grid, 256, router_lds<32, 8>(), st>>>(x, Wr, T, H, E, part, q, qs, qsum);
+        router_logits_kernel<32, 8, 256, 1, 256><<<grid, 256, router_lds<32, 8, 256>(), st>>>(x, Wr, T, H, E, part, q,
+                                                                                             qs, qsum);
     } else {
         const dim3 grid(E / 64, (T + 63) / 64, ROUTER_KC);
-        router_logits_kernel<64, 64, 512><<<grid, 512, router_lds<64, 64>(), st>>>(x, Wr, T, H, E, part, q, qs,
-                                                                                   qsum);
+        router_logits_kernel<64, 64, 512, 2, 128><<<grid, 512, router_lds<64, 64, 128>(), st>>>(x, Wr, T, H, E, part,
+                                                                                                q, qs, qsum);
     }
     return hipGetLastError();
 }
