@@ -48,7 +48,11 @@ __global__ void __launch_bounds__(NT) router_logits_kernel(const float* __restri
     extern __shared__ __align__(16) float rl[];
     float* xs = rl;                       // [TT][RS]
     float* ws = rl + TT * RS;             // [EW][RS]: Wr slice transposed, k contiguous per expert
-    const int e0 = blockIdx.x * EW, t0 = blockIdx.y * TT, c = blockIdx.z;
+    // XCD-aware: workgroups go round-robin over the 8 XCDs, so expert slice (bx % 8) G/8 + bx / 8 puts G/8
+    // neighbouring slices on one XCD -- at 8 experts per slice the 4 slices of a 128-byte Wr row segment then share
+    // that XCD's L2 instead of each XCD fetching the segment
+    const int G = gridDim.x, bx = blockIdx.x;
+    const int e0 = (G % 8 ? bx : (bx % 8) * (G / 8) + bx / 8) * EW, t0 = blockIdx.y * TT, c = blockIdx.z;
     const int tid = threadIdx.x;
     // thread (token group tg, expert group eg): tokens tg TPT + i, experts j EG + eg (consecutive rows of the Wr
     // slice across a wave's lanes: conflict-free), one fma chain each over the chunk's k ascending
