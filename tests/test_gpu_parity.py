@@ -208,6 +208,8 @@ def test_layer_forward_matches_oracle(gpu, T, mix, shared, pool):
     (128, 6, 32, 256),    # decode, no pool
     (64, 8, 100, 48),     # several routing blocks, tiled experts
     (128, 2, 200, 256),
+    (192, 8, 32, 48),     # 24 decode expert slices (3 per XCD), 3 wide router tiles
+    (192, 8, 70, 256),
 ])
 def test_other_expert_counts(gpu, E, K, T, pool):
     """The ABI's other shapes (E a multiple of 64 up to 256, top_k <= 8): every stage bit-exact."""
