@@ -19,6 +19,9 @@ using namespace llmoe;
 
 namespace {
 
+// bytes of each down unit the decode gate_up GEMM requests ahead when its units fit one round
+constexpr int DOWN_PF_BYTES = 48 * 1024;
+
 thread_local std::string g_err;
 
 int fail(int code, const char* fmt, ...) {
@@ -520,7 +523,8 @@ int experts_impl(llmoe_layer* L, const int8_t* xq, const float* xs, const int32_
     if (plan) {
         const DecodePlanArgs pa{T, d.n_experts, K, L->tmask, L->tcopy, L->topk, L->topw,
                                 DispatchOut{d.has_shared, 16, L->bits_d, L->count, L->start, L->units_gu, L->units_dn,
-                                            L->n_units, L->slot_token, L->slot_weight, L->tok_slots}};
+                                            L->n_units, L->slot_token, L->slot_weight, L->tok_slots},
+                                L->d_off_d, DOWN_PF_BYTES};
         L->last_pa = pa;
         L->last_pa.tmask = L->tcopy;   // a re-launch plans from the copy
         HIPCHECK(launch_expert_gemm_plan(g, pa, st));

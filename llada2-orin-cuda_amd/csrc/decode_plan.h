@@ -197,6 +197,8 @@ struct DecodePlanArgs {   // the self-planning gate_up GEMM's routing inputs and
     const int32_t* topk;
     const float* topw;
     DispatchOut d;
+    const uint64_t* d_off;   // [E + 1] down matrix offsets (the down units' weights requested ahead)
+    int pf_bytes;            // bytes of each down unit requested by the workgroups with no second gate_up unit
 };
 
 // the token of slot (it.slot0 + n) of a decode unit, from the plan: the (16 j + n)-th token of the expert's mask for
